@@ -1,0 +1,136 @@
+// C++20 interface to the MI355X decode-attention kernels: the reference's src/metal_attn.hpp
+// (lines 11-108) with the same names, argument meaning and exceptions, implemented over the C ABI
+// of include/kvb_hip.h. Tests and benchmarks stay ordinary C++.
+#pragma once
+
+#include <cstddef>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "kvb/layout.hpp"
+#include "kvb_hip.h"
+
+namespace kvb {
+
+bool gpu_available();
+// The reference's name for gpu_available() (src/metal_attn.hpp:13), kept so callers switch over unchanged.
+inline bool metal_available() { return gpu_available(); }
+std::string device_name();
+
+// Device memory in HBM with a host mirror. The reference's Buffer is shared CPU/GPU storage
+// (src/metal_attn.hpp:16-33); on a discrete GPU the two copies are kept in step here: data()/as()
+// give the host copy for reading and writing (fetching the device copy first if a kernel wrote it
+// since), and the run_* calls upload host writes before launching. So "fill on the host, run,
+// read on the host" works as with the reference, and a timed loop that does not touch data()
+// moves no bytes over PCIe. The host copy is allocated on first use.
+class Buffer {
+public:
+    explicit Buffer(size_t bytes);
+    ~Buffer();
+    Buffer(const Buffer&) = delete;
+    Buffer& operator=(const Buffer&) = delete;
+    void* data() const;                // host copy, may be written: the device copy is refreshed before the next kernel
+    const void* host() const;          // host copy, read only (no upload follows)
+    size_t size() const { return bytes_; }
+    template <class T> T* as() const { return static_cast<T*>(data()); }
+    void* handle() const { return dev_; }  // device pointer
+    // For the launch code: uploads pending host writes and returns the device pointer; after a kernel
+    // writes the buffer, mark_device_written() makes the next host access fetch it.
+    void* device() const;
+    void mark_device_written() const;
+
+private:
+    enum State { kZero, kHostNewer, kSynced, kDeviceNewer };
+    void ensure_host() const;
+    void* dev_ = nullptr;
+    size_t bytes_ = 0;
+    mutable std::unique_ptr<unsigned char[]> host_;
+    mutable State state_ = kZero;  // kZero: neither copy written yet (both read as zeros)
+};
+
+// i8: int8 values with one fp32 scale per (block, KV head) for K and V (quantize_to_paged_i8).
+enum class KvType { f32, f16, i8 };
+inline const char* name(KvType t) { return t == KvType::f32 ? "f32" : t == KvType::f16 ? "f16" : "i8"; }
+inline size_t elem_size(KvType t) { return t == KvType::f32 ? 4 : t == KvType::f16 ? 2 : 1; }
+
+constexpr int kSimdGroups = 4;  // wave64s per paged_decode workgroup (the reference's simdgroups)
+
+// Split-K partition size used when PagedArgs::part_tokens is 0 (src/metal_attn.hpp:43-51): the
+// largest power of two in [64, 512] that still yields at least 512 (sequence, KV head,
+// partition) triples.
+inline int auto_part_tokens(const Shape& s, int max_len) {
+    int part = 512;
+    while (part > 64 && size_t(s.batch) * s.num_kv_heads * ((max_len + part - 1) / part) < 512) part /= 2;
+    return part;
+}
+
+// The MI355X partition policy: the largest power of two in [min_part, max_part] whose workgroup
+// count B * ceil(H / qg) * ceil(max_len / part) still reaches `min_groups` (by default 4 per CU of
+// a 256-CU MI355X); longer partitions mean fewer partial results to merge, more workgroups keep
+// more bytes in flight. qg is the number of query heads one workgroup serves.
+int mi355x_part_tokens(const Shape& s, int max_len, int min_groups = 1024, int min_part = 256, int max_part = 4096);
+
+struct PagedArgs {
+    Shape shape;
+    KvType type = KvType::f32;
+    int page_size = 16;
+    int max_blocks = 0;      // PagedLayout::max_blocks
+    int max_len = 0;         // longest sequence, sizes the split-K workspace; 0: all empty, out is 0
+    int part_tokens = 0;     // split-K partition size, 0 = auto_part_tokens()
+    const Buffer* q;         // float [B][H][D]
+    const Buffer* k;         // type  [blocks][Hkv][page][D]
+    const Buffer* v;
+    const Buffer* block_table;  // int32 [B][max_blocks]
+    const Buffer* seq_lens;     // int32 [B]
+    const Buffer* out;          // float [B][H][D]
+    bool share_kv = true;       // false: one workgroup per query head (GQA ablation)
+    const Buffer* k_scale = nullptr;  // float [blocks][Hkv], required for KvType::i8
+    const Buffer* v_scale = nullptr;
+    const Buffer* workspace = nullptr;  // optional split-K workspace (kvb_paged_workspace_bytes)
+};
+
+struct NaiveArgs {
+    Shape shape;
+    KvType type = KvType::f32;
+    int max_len = 0;  // row stride of the contiguous cache
+    const Buffer* q;
+    const Buffer* k;  // type [B][Hkv][max_len][D]
+    const Buffer* v;
+    const Buffer* seq_lens;
+    const Buffer* out;
+};
+
+// Each call queues the kernels on one stream, waits, and returns their GPU time in milliseconds
+// (a hipEvent pair). Throws std::invalid_argument, before any GPU work, for a sequence length below
+// 0, above max_len, or (paged) above max_blocks * page_size, and for the other refusals of
+// kvb_run_paged; std::runtime_error for device failures (src/metal_attn.hpp:82-87).
+double run_paged(const PagedArgs&);
+double run_naive(const NaiveArgs&);
+
+// `steps` decode steps on the same inputs, back to back on one stream (src/metal_attn.hpp:89-91).
+double run_paged_steps(const PagedArgs&, int steps);
+
+// One decode step with the GPU time of each kernel.
+struct KernelTimes {
+    double decode_ms = 0, reduce_ms = 0;
+};
+KernelTimes run_paged_split(const PagedArgs&);
+
+// Between begin_pipelined() and end_pipelined(), run_*() and flush_gpu_caches() queue their work
+// without waiting (run_*() return 0); end_pipelined() waits and returns the GPU time of every
+// run_*() call in order (src/metal_attn.hpp:93-99). On one HIP stream the runs execute one at a
+// time, back to back.
+void begin_pipelined();
+std::vector<double> end_pipelined();
+
+// Reads `src` once with a streaming kernel over every CU; returns GPU milliseconds.
+double run_read_bandwidth(const Buffer& src);
+
+// Overwrites a 1 GiB scratch buffer, more than the MALL and L2s hold, so the next run starts cold.
+void flush_gpu_caches();
+
+// The C ABI view of `a` (device pointers resolved, host writes uploaded).
+kvb_paged_args c_args(const PagedArgs& a);
+
+}  // namespace kvb

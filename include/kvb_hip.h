@@ -1,0 +1,151 @@
+/*
+ * kvb_hip.h -- C ABI of libkvb_hip.so, the MI355X (gfx950) paged-KV decode-attention library.
+ *
+ * This is the drop-in boundary: it replaces the Objective-C++/Metal host layer behind the
+ * reference's C++ interface (chipontix/kv-cache-bench src/metal_attn.hpp:11-108, implemented in
+ * src/metal_attn.mm). Every entry point takes plain pointers and sizes; device pointers come
+ * from kvb_buffer_alloc (or any hipMalloc'd memory of the current device). Calls are
+ * single-threaded and not reentrant, like the reference (src/metal_attn.mm:40-42).
+ *
+ * Status codes: KVB_OK, KVB_EINVAL (bad arguments, refused before any GPU work: the reference's
+ * std::invalid_argument), KVB_ERUNTIME (a HIP failure: std::runtime_error), KVB_ENODEV (no GPU:
+ * the reference's metal_available() == false, exit code 77 in its tests). kvb_last_error()
+ * describes the last failing call.
+ */
+#ifndef KVB_HIP_H
+#define KVB_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { KVB_OK = 0, KVB_EINVAL = 1, KVB_ERUNTIME = 2, KVB_ENODEV = 3 };
+
+/* KV storage types (KvType, src/metal_attn.hpp:35-39). I8 carries one fp32 scale per
+ * (physical block, KV head) for K and one for V. */
+enum { KVB_KV_F32 = 0, KVB_KV_F16 = 1, KVB_KV_I8 = 2 };
+
+/* ---- device ------------------------------------------------------------------------------ */
+
+/* 1 if a HIP device is present (metal_available, src/metal_attn.hpp:13). */
+int kvb_gpu_available(void);
+/* Device name into buf (device_name, src/metal_attn.hpp:14). */
+int kvb_device_name(char* buf, size_t cap);
+/* Message of the last call that did not return KVB_OK ("" if none). */
+const char* kvb_last_error(void);
+/* Runs the library's work on `stream` (a hipStream_t; NULL = the library's own stream, created
+ * at default priority). Timing events are recorded on the same stream. No reference counterpart:
+ * lets a caller that owns a stream (a serving loop, PyTorch) order decode steps with its own work. */
+int kvb_set_stream(void* stream);
+/* Waits for all work the library has queued. */
+int kvb_synchronize(void);
+
+/* ---- memory (Buffer, src/metal_attn.hpp:16-33) ------------------------------------------- */
+/* The reference's Buffer is shared CPU/GPU storage; on MI355X the device copy lives in HBM and
+ * the C++ host layer keeps a host mirror, moved with these copies. */
+int kvb_buffer_alloc(void** dev, size_t bytes); /* min 16 bytes, like src/metal_attn.mm:142 */
+int kvb_buffer_free(void* dev);
+int kvb_copy_h2d(void* dev, const void* host, size_t bytes);
+int kvb_copy_d2h(void* host, const void* dev, size_t bytes);
+int kvb_fill_bytes(void* dev, int value, size_t bytes);
+
+/* ---- paged decode (PagedArgs, src/metal_attn.hpp:53-69) ---------------------------------- */
+typedef struct kvb_paged_args {
+    int batch;        /* B: sequences, one new query token each */
+    int num_heads;    /* H: query heads */
+    int num_kv_heads; /* Hkv: KV heads, H % Hkv == 0; query head h reads KV head h / (H / Hkv) */
+    int head_dim;     /* D: 64 or 128 */
+    int kv_type;      /* KVB_KV_F32 | KVB_KV_F16 | KVB_KV_I8 */
+    int page_size;    /* tokens per physical block */
+    int max_blocks;   /* row stride of block_table */
+    int max_len;      /* longest sequence; sizes the split-K workspace; 0: every output is 0 */
+    int part_tokens;  /* split-K partition size in tokens, 0 = kvb_auto_part_tokens() */
+    int share_kv;     /* 1: one workgroup serves every query head of a KV head (reads K/V once per
+                         group); 0: one workgroup per query head (the GQA ablation) */
+    const float* q;              /* device, float [B][H][D] */
+    const void* k;               /* device, kv_type [blocks][Hkv][page_size][D] */
+    const void* v;               /* device, same layout as k */
+    const int32_t* block_table;  /* device, int32 [B][max_blocks]; logical block i of sequence b
+                                    lives in physical block block_table[b*max_blocks + i] */
+    const int32_t* seq_lens;     /* device, int32 [B] */
+    const int32_t* host_seq_lens;/* host copy of seq_lens, read by the capacity check */
+    float* out;                  /* device, float [B][H][D] */
+    const float* k_scale;        /* device, float [blocks][Hkv]; required for I8 */
+    const float* v_scale;
+    /* Optional caller-owned split-K workspace (NULL: the library's grow-only workspace). Layout:
+     * part_out float [B][H][max_parts][D], then part_ml float2 [B][H][max_parts] = (m, l), with m
+     * the partition's max score (natural-log units) and l its exp-sum; see
+     * kvb_paged_workspace_bytes. Only slots of non-empty partitions are written. */
+    void* workspace;
+    size_t workspace_bytes;
+} kvb_paged_args;
+
+/* Split-K partition size used when part_tokens == 0 (auto_part_tokens, src/metal_attn.hpp:43-51):
+ * the largest power of two in [64, 512] with batch * Hkv * ceil(max_len / part) >= 512. */
+int kvb_auto_part_tokens(int batch, int num_kv_heads, int max_len);
+/* Partitions per (sequence, head) in the workspace: max(1, ceil(max_len / part)) with part
+ * resolved as kvb_run_paged does (src/metal_attn.mm:160-161). Returns -1 on bad arguments. */
+int kvb_paged_max_parts(const kvb_paged_args* a);
+/* Bytes of the workspace a call with these arguments uses (0 on bad arguments). */
+size_t kvb_paged_workspace_bytes(const kvb_paged_args* a);
+
+/* The refusals of kvb_run_paged alone (KVB_OK or KVB_EINVAL): reads only host_seq_lens and the
+ * sizes, needs no GPU. Lets a host layer refuse before it uploads anything. */
+int kvb_check_paged(const kvb_paged_args* a);
+
+/* One decode step: paged_decode then paged_reduce on one stream (run_paged, src/metal_attn.hpp:86).
+ * *ms = GPU time from before the first kernel to after the last (hipEvent pair); 0 in pipelined
+ * mode. Refuses (KVB_EINVAL, before any GPU work, output untouched) part_tokens < 0, max_len < 0,
+ * page_size <= 0, I8 without scales, a length < 0 or > max_len or > max_blocks * page_size,
+ * head_dim not 64/128, H % Hkv != 0 (src/metal_attn.mm:72-73, 107-117, 199-201). */
+int kvb_run_paged(const kvb_paged_args* a, double* ms);
+/* `steps` decode steps on the same inputs, back to back on one stream, one event pair around them
+ * (run_paged_steps, src/metal_attn.hpp:91). */
+int kvb_run_paged_steps(const kvb_paged_args* a, int steps, double* ms);
+/* One synchronous decode step timed per kernel: *decode_ms and *reduce_ms are the hipEvent times
+ * of paged_decode and of paged_reduce. Not in the reference (its timing is per command buffer,
+ * src/metal_attn.mm:119-130); used to price the decode kernel against its roofline. */
+int kvb_run_paged_split(const kvb_paged_args* a, double* decode_ms, double* reduce_ms);
+
+/* ---- naive 3-pass baseline (NaiveArgs / run_naive, src/metal_attn.hpp:71-87) ------------- */
+typedef struct kvb_naive_args {
+    int batch, num_heads, num_kv_heads, head_dim;
+    int kv_type;                 /* KVB_KV_F32 or KVB_KV_F16 */
+    int max_len;                 /* row stride of the contiguous cache */
+    const float* q;              /* device, float [B][H][D] */
+    const void* k;               /* device, kv_type [B][Hkv][max_len][D] */
+    const void* v;
+    const int32_t* seq_lens;     /* device, int32 [B] */
+    const int32_t* host_seq_lens;/* host copy of seq_lens */
+    float* out;                  /* device, float [B][H][D] */
+} kvb_naive_args;
+/* scores -> softmax -> PV with the scores in global memory. Refuses I8 and lengths < 0 or
+ * > max_len (src/metal_attn.mm:211-247). */
+int kvb_run_naive(const kvb_naive_args* a, double* ms);
+/* The refusals of kvb_run_naive alone. */
+int kvb_check_naive(const kvb_naive_args* a);
+
+/* ---- timing modes (src/metal_attn.hpp:93-99) --------------------------------------------- */
+/* Between begin and end, run_* queue their work without waiting and return 0; end waits and
+ * writes the GPU time of each timed run_* call in order (up to cap values, *count = number of
+ * runs). The flush is queued but not timed, as in src/metal_attn.mm:266-276. */
+int kvb_begin_pipelined(void);
+/* Timed runs queued since kvb_begin_pipelined (the size end_pipelined needs). */
+size_t kvb_pipelined_pending(void);
+int kvb_end_pipelined(double* ms, size_t cap, size_t* count);
+
+/* ---- probes ------------------------------------------------------------------------------ */
+/* Streams `bytes` (a multiple of 16) of `dev` once with 128-bit loads over every CU; *ms is the
+ * kernel's GPU time (run_read_bandwidth, src/metal_attn.hpp:102). */
+int kvb_run_read_bandwidth(const void* dev, size_t bytes, double* ms);
+/* Overwrites a 1 GiB scratch buffer (more than the 256 MB MALL plus the L2s) so the next timed
+ * run starts cold (flush_gpu_caches, src/metal_attn.hpp:106; the reference's is 256 MiB). */
+int kvb_flush_gpu_caches(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KVB_HIP_H */

@@ -1,0 +1,154 @@
+// paged_reduce, the naive three-pass baseline, the read-bandwidth probe and the cache-flush fill.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "kvb_kernels.hpp"
+
+namespace kvbk {
+namespace {
+
+constexpr float kNegBigR = -1e30f;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Merges the partitions of one (sequence, query head) (src/kernels.metal:123-147): weights
+// l_i * exp(m_i - M) over the ceil(len / part) written slots; an empty sequence gives exactly 0.
+// Grid (H, B), D threads: each thread owns one output element.
+template <int D>
+__global__ __launch_bounds__(D) void paged_reduce_kernel(ReduceParams p) {
+    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x, H = p.num_heads;
+    const int parts = (p.seq_lens[b] + p.part_tokens - 1) / p.part_tokens;
+    float* o = p.out + ((size_t)b * H + h) * D;
+    if (parts <= 0) {
+        o[d] = 0.0f;
+        return;
+    }
+    const size_t base = ((size_t)b * H + h) * p.max_parts;
+    float M = kNegBigR;
+    for (int i = 0; i < parts; ++i) M = fmaxf(M, p.part_ml[base + i].x);
+    float L = 0.0f, acc = 0.0f;
+    for (int i = 0; i < parts; ++i) {
+        const float2 ml = p.part_ml[base + i];
+        const float w = ml.y * __builtin_amdgcn_exp2f((ml.x - M) * kLog2e);
+        L += w;
+        acc += w * p.part_out[(base + i) * D + d];
+    }
+    o[d] = acc / L;
+}
+
+template <int KIND>
+__device__ __forceinline__ float kv_at(const void* base, size_t i) {
+    if constexpr (KIND == KV_F16) return (float)static_cast<const _Float16*>(base)[i];
+    else return static_cast<const float*>(base)[i];
+}
+
+// One thread per (t, h, b): scores[b][h][t] = scale * q . k_t (src/kernels.metal:152-166).
+template <int KIND>
+__global__ __launch_bounds__(256) void naive_scores_kernel(NaiveParams p, int D, int G) {
+    const int t = blockIdx.x * 256 + threadIdx.x, h = blockIdx.y, b = blockIdx.z, H = p.num_heads;
+    if (t >= p.seq_lens[b]) return;
+    const size_t krow = (((size_t)b * p.num_kv_heads + h / G) * p.max_len + t) * D;
+    const float* qh = p.q + ((size_t)b * H + h) * D;
+    float s = 0.0f;
+    for (int d = 0; d < D; ++d) s += qh[d] * kv_at<KIND>(p.k, krow + d);
+    p.scores[((size_t)b * H + h) * p.max_len + t] = s * p.scale;
+}
+
+// One workgroup of 256 threads per (h, b): max, exp-sum, normalise in place (src/kernels.metal:168-203).
+__global__ __launch_bounds__(256) void naive_softmax_kernel(NaiveParams p) {
+    __shared__ float red[256];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, len = p.seq_lens[b];
+    float* row = p.scores + ((size_t)b * p.num_heads + h) * p.max_len;
+    float mx = kNegBigR;
+    for (int t = tid; t < len; t += 256) mx = fmaxf(mx, row[t]);
+    red[tid] = mx;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
+        __syncthreads();
+    }
+    mx = red[0];
+    __syncthreads();
+    float sum = 0.0f;
+    for (int t = tid; t < len; t += 256) {
+        const float e = __expf(row[t] - mx);
+        row[t] = e;
+        sum += e;
+    }
+    red[tid] = sum;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (tid < s) red[tid] += red[tid + s];
+        __syncthreads();
+    }
+    const float inv = 1.0f / red[0];
+    for (int t = tid; t < len; t += 256) row[t] *= inv;
+}
+
+// One thread per (d, h, b): out[b][h][d] = sum_t p_t v_t[d] (src/kernels.metal:205-218).
+template <int KIND>
+__global__ void naive_pv_kernel(NaiveParams p, int D, int G) {
+    const int d = threadIdx.x, h = blockIdx.x, b = blockIdx.y, H = p.num_heads, len = p.seq_lens[b];
+    const float* pr = p.scores + ((size_t)b * H + h) * p.max_len;
+    const size_t vbase = ((size_t)b * p.num_kv_heads + h / G) * p.max_len * D + d;
+    float o = 0.0f;
+    for (int t = 0; t < len; ++t) o += pr[t] * kv_at<KIND>(p.v, vbase + (size_t)t * D);
+    p.out[((size_t)b * H + h) * D + d] = o;
+}
+
+// Grid-stride streaming read with 8 independent 16-byte loads in flight per lane
+// (src/kernels.metal:220-233). XOR-accumulated; the store fires only on a sentinel no real
+// buffer of the probe (all words equal) produces.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void read_bw_kernel(const u32x4_t* __restrict__ src, size_t n16, float* sink) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * 256;
+    uint32_t acc = 0;
+    for (; i + 7 * stride < n16; i += 8 * stride) {
+        u32x4_t x[8];
+        for (int u = 0; u < 8; ++u) x[u] = __builtin_nontemporal_load(src + i + u * stride);
+        for (int u = 0; u < 8; ++u) acc ^= x[u].x ^ x[u].y ^ x[u].z ^ x[u].w;
+    }
+    for (; i < n16; i += stride) {
+        const u32x4_t x = src[i];
+        acc ^= x.x ^ x.y ^ x.z ^ x.w;
+    }
+    if (acc == 0x9e3779b9u) sink[(size_t)blockIdx.x * 256 + threadIdx.x] = 1.0f;
+}
+
+__global__ __launch_bounds__(256) void fill_kernel(uint4* dst, size_t n16, uint32_t value) {
+    const uint4 v = make_uint4(value, value, value, value);
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256) dst[i] = v;
+}
+
+}  // namespace
+
+hipError_t launch_paged_reduce(int head_dim, const ReduceParams& p, int batch, hipStream_t s) {
+    const dim3 grid(p.num_heads, batch);
+    if (head_dim == 64) hipLaunchKernelGGL(paged_reduce_kernel<64>, grid, dim3(64), 0, s, p);
+    else if (head_dim == 128) hipLaunchKernelGGL(paged_reduce_kernel<128>, grid, dim3(128), 0, s, p);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_naive(int kind, int head_dim, int group, const NaiveParams& p, int batch, hipStream_t s) {
+    const dim3 sgrid((unsigned)((p.max_len > 0 ? p.max_len : 1) + 255) / 256, p.num_heads, batch);
+    if (kind == KV_F16) hipLaunchKernelGGL(naive_scores_kernel<KV_F16>, sgrid, dim3(256), 0, s, p, head_dim, group);
+    else hipLaunchKernelGGL(naive_scores_kernel<KV_F32>, sgrid, dim3(256), 0, s, p, head_dim, group);
+    hipLaunchKernelGGL(naive_softmax_kernel, dim3(p.num_heads, batch), dim3(256), 0, s, p);
+    if (kind == KV_F16) hipLaunchKernelGGL(naive_pv_kernel<KV_F16>, dim3(p.num_heads, batch), dim3(head_dim), 0, s, p, head_dim, group);
+    else hipLaunchKernelGGL(naive_pv_kernel<KV_F32>, dim3(p.num_heads, batch), dim3(head_dim), 0, s, p, head_dim, group);
+    return hipGetLastError();
+}
+
+hipError_t launch_read_bw(const void* src, size_t n16, float* sink, hipStream_t s) {
+    hipLaunchKernelGGL(read_bw_kernel, dim3(2048), dim3(256), 0, s, static_cast<const u32x4_t*>(src), n16, sink);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill(void* dst, size_t n16, uint32_t value, hipStream_t s) {
+    hipLaunchKernelGGL(fill_kernel, dim3(2048), dim3(256), 0, s, static_cast<uint4*>(dst), n16, value);
+    return hipGetLastError();
+}
+
+}  // namespace kvbk

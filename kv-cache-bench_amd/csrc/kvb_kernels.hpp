@@ -1,0 +1,79 @@
+// Launch parameters and launcher declarations shared by the gfx950 kernels and the runtime.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace kvbk {
+
+enum KvKind { KV_F32 = 0, KV_F16 = 1, KV_I8 = 2 };
+
+// Waves per paged_decode workgroup (the reference's kSimdGroups, src/metal_attn.hpp:41).
+constexpr int kDecodeWaves = 4;
+// Tokens one wave handles per step of its loop: the N of a 16x16 MFMA tile.
+constexpr int kTile = 16;
+
+struct DecodeParams {
+    const float* q;             // [B][H][D]
+    const void* k;              // [blocks][Hkv][page][D]
+    const void* v;
+    const int32_t* block_table; // [B][max_blocks]
+    const int32_t* seq_lens;    // [B]
+    const float* k_scale;       // [blocks][Hkv], i8 only
+    const float* v_scale;
+    float* part_out;            // [B][H][max_parts][D]: partition output o / l
+    float2* part_ml;            // [B][H][max_parts]: (max score, exp-sum), natural-log units
+    int num_heads;
+    int num_kv_heads;
+    int group;                  // H / Hkv
+    int page_size;
+    int max_blocks;
+    int max_parts;
+    int part_tokens;
+    float qscale;               // softmax scale * log2(e): scores are kept in base-2 units
+};
+
+struct ReduceParams {
+    const float* part_out;
+    const float2* part_ml;
+    const int32_t* seq_lens;
+    float* out;                 // [B][H][D]
+    int num_heads;
+    int max_parts;
+    int part_tokens;
+};
+
+struct NaiveParams {
+    const float* q;
+    const void* k;              // [B][Hkv][max_len][D]
+    const void* v;
+    const int32_t* seq_lens;
+    float* scores;              // [B][H][max_len]
+    float* out;
+    int num_heads;
+    int num_kv_heads;
+    int max_len;
+    float scale;
+};
+
+// paged_decode for one storage kind: grid (max_parts, H / qg, batch), kDecodeWaves waves per
+// workgroup. `fast`: every 16-token tile lies inside one page (page_size % 16 == 0 and
+// part_tokens % 16 == 0), so block ids and scales are read once per tile.
+hipError_t launch_paged_decode_f32(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s);
+hipError_t launch_paged_decode_f16(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s);
+hipError_t launch_paged_decode_i8(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s);
+
+// paged_reduce: grid (H, batch), head_dim threads.
+hipError_t launch_paged_reduce(int head_dim, const ReduceParams& p, int batch, hipStream_t s);
+
+// The naive three-pass baseline over a contiguous cache (f32 or f16).
+hipError_t launch_naive(int kind, int head_dim, int group, const NaiveParams& p, int batch, hipStream_t s);
+
+// Streaming read of n16 16-byte words; the guarded store into sink never fires for real data.
+hipError_t launch_read_bw(const void* src, size_t n16, float* sink, hipStream_t s);
+// Overwrites n16 16-byte words with `value`.
+hipError_t launch_fill(void* dst, size_t n16, uint32_t value, hipStream_t s);
+
+}  // namespace kvbk

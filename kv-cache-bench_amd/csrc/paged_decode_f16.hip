@@ -1,0 +1,11 @@
+// paged_decode instantiations for f16 caches (head_dim 64/128, 1/2/4/8 query heads per workgroup,
+// tile-aligned and any-page variants); one file per storage type so they compile in parallel.
+#include "paged_decode_impl.hpp"
+
+namespace kvbk {
+
+hipError_t launch_paged_decode_f16(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s) {
+    return launch_for_kind<KV_F16>(head_dim, qg, fast, p, batch, s);
+}
+
+}  // namespace kvbk

@@ -1,0 +1,440 @@
+// The C ABI of libkvb_hip.so (include/kvb_hip.h): argument checks, device state, workspaces,
+// launches and hipEvent timing. Plays the part of the reference's Objective-C++ host layer
+// (src/metal_attn.mm): the same refusals before any GPU work, a grow-only split-K workspace, GPU
+// time per submitted step and a pipelined (queue now, collect times later) mode.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "kvb_hip.h"
+#include "kvb_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, std::string msg) {
+    g_err = std::move(msg);
+    return code;
+}
+
+#define KVB_HIP(expr)                                                                         \
+    do {                                                                                      \
+        const hipError_t e_ = (expr);                                                         \
+        if (e_ != hipSuccess) return fail(KVB_ERUNTIME, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+struct Runtime {
+    bool ready = false;
+    int device = -1;
+    hipStream_t own = nullptr;
+    hipStream_t stream = nullptr;
+    void* ws = nullptr;             // split-K workspace (grow-only)
+    size_t ws_bytes = 0;
+    void* scores = nullptr;         // naive scores (grow-only)
+    size_t scores_bytes = 0;
+    void* flush_buf = nullptr;      // cache-flush target
+    float* sink = nullptr;          // read-probe sink
+    uint32_t flush_value = 0;
+    bool pipelined = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> timed;
+    std::vector<hipEvent_t> spare;
+};
+Runtime g;
+
+constexpr size_t kFlushBytes = size_t(1) << 30;
+constexpr size_t kSinkFloats = 2048 * 256;
+
+int ensure_device() {
+    if (g.ready) return KVB_OK;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(KVB_ENODEV, "no HIP device");
+    KVB_HIP(hipGetDevice(&g.device));
+    KVB_HIP(hipStreamCreateWithFlags(&g.own, hipStreamNonBlocking));
+    if (!g.stream) g.stream = g.own;
+    g.ready = true;
+    return KVB_OK;
+}
+
+int get_event(hipEvent_t* e) {
+    if (!g.spare.empty()) {
+        *e = g.spare.back();
+        g.spare.pop_back();
+        return KVB_OK;
+    }
+    KVB_HIP(hipEventCreate(e));
+    return KVB_OK;
+}
+
+// Grows a library-owned buffer; waits for queued work first, since it may still use the old one.
+int grow(void** buf, size_t* have, size_t need) {
+    if (*have >= need && *buf) return KVB_OK;
+    KVB_HIP(hipStreamSynchronize(g.stream));
+    if (*buf) KVB_HIP(hipFree(*buf));
+    *buf = nullptr;
+    *have = 0;
+    KVB_HIP(hipMalloc(buf, std::max<size_t>(need, 256)));
+    *have = std::max<size_t>(need, 256);
+    return KVB_OK;
+}
+
+// Ends a timed submission: queue the pair (pipelined) or wait and report its GPU time.
+int finish(hipEvent_t e0, hipEvent_t e1, double* ms) {
+    if (g.pipelined) {
+        g.timed.emplace_back(e0, e1);
+        if (ms) *ms = 0.0;
+        return KVB_OK;
+    }
+    KVB_HIP(hipEventSynchronize(e1));
+    float f = 0.0f;
+    KVB_HIP(hipEventElapsedTime(&f, e0, e1));
+    g.spare.push_back(e0);
+    g.spare.push_back(e1);
+    if (ms) *ms = f;
+    return KVB_OK;
+}
+
+int resolve_part(const kvb_paged_args* a) {
+    return a->part_tokens ? a->part_tokens : kvb_auto_part_tokens(a->batch, a->num_kv_heads, a->max_len);
+}
+
+int max_parts_of(const kvb_paged_args* a) {
+    const int part = resolve_part(a);
+    return std::max(1, (int)(((long long)a->max_len + part - 1) / part));
+}
+
+size_t workspace_need(const kvb_paged_args* a) {
+    const size_t slots = (size_t)a->batch * a->num_heads * (size_t)max_parts_of(a);
+    return slots * (size_t)a->head_dim * sizeof(float) + slots * sizeof(float2);
+}
+
+int check_lens(int batch, const int32_t* lens, int max_len, size_t capacity) {
+    for (int b = 0; b < batch; ++b) {
+        const int len = lens[b];
+        if (len < 0 || len > max_len || (size_t)len > capacity)
+            return fail(KVB_EINVAL, "sequence " + std::to_string(b) + " has length " + std::to_string(len) +
+                                        ", max_len " + std::to_string(max_len) + ", capacity " +
+                                        std::to_string(capacity));
+    }
+    return KVB_OK;
+}
+
+int check_shape(int batch, int H, int Hkv, int D) {
+    if (batch < 0 || H <= 0 || Hkv <= 0) return fail(KVB_EINVAL, "batch < 0 or a head count <= 0");
+    if (D != 64 && D != 128) return fail(KVB_EINVAL, "head_dim must be 64 or 128");
+    if (H % Hkv != 0) return fail(KVB_EINVAL, "H % Hkv != 0");
+    return KVB_OK;
+}
+
+// Every refusal of run_paged (src/metal_attn.mm:72-73, 107-117, 199-201), host-side only.
+int validate_paged(const kvb_paged_args* a) {
+    if (!a) return fail(KVB_EINVAL, "null arguments");
+    if (a->part_tokens < 0 || a->max_len < 0 || a->page_size <= 0)
+        return fail(KVB_EINVAL, "part_tokens < 0, max_len < 0 or page_size <= 0");
+    if (a->kv_type < KVB_KV_F32 || a->kv_type > KVB_KV_I8) return fail(KVB_EINVAL, "unknown kv_type");
+    if (a->kv_type == KVB_KV_I8 && (!a->k_scale || !a->v_scale)) return fail(KVB_EINVAL, "i8 cache without scales");
+    if (int st = check_shape(a->batch, a->num_heads, a->num_kv_heads, a->head_dim)) return st;
+    if (a->max_blocks < 0) return fail(KVB_EINVAL, "max_blocks < 0");
+    if (a->batch > 0 && !a->host_seq_lens) return fail(KVB_EINVAL, "host_seq_lens is required");
+    if (int st = check_lens(a->batch, a->host_seq_lens, a->max_len, (size_t)a->max_blocks * (size_t)a->page_size)) return st;
+    if (a->batch > 0 && (!a->q || !a->k || !a->v || !a->seq_lens || !a->out || (a->max_blocks > 0 && !a->block_table)))
+        return fail(KVB_EINVAL, "null device pointer");
+    if (a->workspace && a->workspace_bytes < workspace_need(a))
+        return fail(KVB_EINVAL, "workspace smaller than kvb_paged_workspace_bytes()");
+    return KVB_OK;
+}
+
+int query_heads_per_group(const kvb_paged_args* a) {
+    const int G = a->num_heads / a->num_kv_heads;
+    if (!a->share_kv) return 1;
+    return G % 8 == 0 ? 8 : G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
+}
+
+// Queues one decode step (paged_decode then paged_reduce); e_mid, if given, is recorded between.
+int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, hipEvent_t e_mid) {
+    const int part = resolve_part(a);
+    const int qg = query_heads_per_group(a);
+    kvbk::DecodeParams p{};
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.block_table = a->block_table;
+    p.seq_lens = a->seq_lens;
+    p.k_scale = a->k_scale;
+    p.v_scale = a->v_scale;
+    p.part_out = part_out;
+    p.part_ml = part_ml;
+    p.num_heads = a->num_heads;
+    p.num_kv_heads = a->num_kv_heads;
+    p.group = a->num_heads / a->num_kv_heads;
+    p.page_size = a->page_size;
+    p.max_blocks = a->max_blocks;
+    p.max_parts = max_parts_of(a);
+    p.part_tokens = part;
+    p.qscale = (1.0f / std::sqrt((float)a->head_dim)) * 1.4426950408889634f;
+    const bool fast = a->page_size % kvbk::kTile == 0 && part % kvbk::kTile == 0;
+    hipError_t e = hipSuccess;
+    switch (a->kv_type) {
+        case KVB_KV_F32: e = kvbk::launch_paged_decode_f32(a->head_dim, qg, fast, p, a->batch, g.stream); break;
+        case KVB_KV_F16: e = kvbk::launch_paged_decode_f16(a->head_dim, qg, fast, p, a->batch, g.stream); break;
+        default: e = kvbk::launch_paged_decode_i8(a->head_dim, qg, fast, p, a->batch, g.stream); break;
+    }
+    if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("paged_decode launch: ") + hipGetErrorString(e));
+    if (e_mid) KVB_HIP(hipEventRecord(e_mid, g.stream));
+    kvbk::ReduceParams r{part_out, part_ml, a->seq_lens, a->out, a->num_heads, p.max_parts, part};
+    e = kvbk::launch_paged_reduce(a->head_dim, r, a->batch, g.stream);
+    if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("paged_reduce launch: ") + hipGetErrorString(e));
+    return KVB_OK;
+}
+
+int workspace_for(const kvb_paged_args* a, float** part_out, float2** part_ml) {
+    const size_t slots = (size_t)a->batch * a->num_heads * (size_t)max_parts_of(a);
+    char* base = nullptr;
+    if (a->workspace) {
+        base = static_cast<char*>(a->workspace);
+    } else {
+        if (int st = grow(&g.ws, &g.ws_bytes, workspace_need(a))) return st;
+        base = static_cast<char*>(g.ws);
+    }
+    *part_out = reinterpret_cast<float*>(base);
+    *part_ml = reinterpret_cast<float2*>(base + slots * (size_t)a->head_dim * sizeof(float));
+    return KVB_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kvb_gpu_available(void) {
+    int n = 0;
+    return hipGetDeviceCount(&n) == hipSuccess && n > 0;
+}
+
+int kvb_device_name(char* buf, size_t cap) {
+    if (!buf || cap == 0) return fail(KVB_EINVAL, "null buffer");
+    buf[0] = '\0';
+    if (int st = ensure_device()) return st;
+    hipDeviceProp_t prop;
+    KVB_HIP(hipGetDeviceProperties(&prop, g.device));
+    std::snprintf(buf, cap, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
+    return KVB_OK;
+}
+
+const char* kvb_last_error(void) { return g_err.c_str(); }
+
+int kvb_set_stream(void* stream) {
+    if (int st = ensure_device()) return st;
+    g.stream = stream ? static_cast<hipStream_t>(stream) : g.own;
+    return KVB_OK;
+}
+
+int kvb_synchronize(void) {
+    if (int st = ensure_device()) return st;
+    KVB_HIP(hipStreamSynchronize(g.stream));
+    return KVB_OK;
+}
+
+int kvb_buffer_alloc(void** dev, size_t bytes) {
+    if (!dev) return fail(KVB_EINVAL, "null output pointer");
+    *dev = nullptr;
+    if (int st = ensure_device()) return st;
+    KVB_HIP(hipMalloc(dev, std::max<size_t>(bytes, 16)));
+    return KVB_OK;
+}
+
+int kvb_buffer_free(void* dev) {
+    if (!dev) return KVB_OK;
+    if (int st = ensure_device()) return st;
+    KVB_HIP(hipStreamSynchronize(g.stream));
+    KVB_HIP(hipFree(dev));
+    return KVB_OK;
+}
+
+int kvb_copy_h2d(void* dev, const void* host, size_t bytes) {
+    if (bytes == 0) return KVB_OK;
+    if (!dev || !host) return fail(KVB_EINVAL, "null pointer");
+    if (int st = ensure_device()) return st;
+    KVB_HIP(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, g.stream));
+    KVB_HIP(hipStreamSynchronize(g.stream));
+    return KVB_OK;
+}
+
+int kvb_copy_d2h(void* host, const void* dev, size_t bytes) {
+    if (bytes == 0) return KVB_OK;
+    if (!dev || !host) return fail(KVB_EINVAL, "null pointer");
+    if (int st = ensure_device()) return st;
+    KVB_HIP(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, g.stream));
+    KVB_HIP(hipStreamSynchronize(g.stream));
+    return KVB_OK;
+}
+
+int kvb_fill_bytes(void* dev, int value, size_t bytes) {
+    if (bytes == 0) return KVB_OK;
+    if (!dev) return fail(KVB_EINVAL, "null pointer");
+    if (int st = ensure_device()) return st;
+    KVB_HIP(hipMemsetAsync(dev, value, bytes, g.stream));
+    KVB_HIP(hipStreamSynchronize(g.stream));
+    return KVB_OK;
+}
+
+int kvb_auto_part_tokens(int batch, int num_kv_heads, int max_len) {
+    int part = 512;
+    while (part > 64 && (size_t)batch * num_kv_heads * (size_t)((max_len + part - 1) / part) < 512) part /= 2;
+    return part;
+}
+
+int kvb_paged_max_parts(const kvb_paged_args* a) {
+    if (!a || a->part_tokens < 0 || a->max_len < 0 || a->batch < 0 || a->num_kv_heads <= 0) return -1;
+    return max_parts_of(a);
+}
+
+size_t kvb_paged_workspace_bytes(const kvb_paged_args* a) {
+    if (!a || a->part_tokens < 0 || a->max_len < 0 || a->batch < 0 || a->num_heads <= 0 || a->num_kv_heads <= 0 ||
+        (a->head_dim != 64 && a->head_dim != 128))
+        return 0;
+    return workspace_need(a);
+}
+
+int kvb_check_paged(const kvb_paged_args* a) { return validate_paged(a); }
+
+int kvb_run_paged_steps(const kvb_paged_args* a, int steps, double* ms) {
+    if (ms) *ms = 0.0;
+    if (int st = validate_paged(a)) return st;
+    if (steps < 0) return fail(KVB_EINVAL, "steps < 0");
+    if (int st = ensure_device()) return st;
+    if (a->batch == 0 || steps == 0) return KVB_OK;
+    float* part_out = nullptr;
+    float2* part_ml = nullptr;
+    if (int st = workspace_for(a, &part_out, &part_ml)) return st;
+    hipEvent_t e0, e1;
+    if (int st = get_event(&e0)) return st;
+    if (int st = get_event(&e1)) return st;
+    KVB_HIP(hipEventRecord(e0, g.stream));
+    for (int i = 0; i < steps; ++i)
+        if (int st = enqueue_paged(a, part_out, part_ml, nullptr)) return st;
+    KVB_HIP(hipEventRecord(e1, g.stream));
+    return finish(e0, e1, ms);
+}
+
+int kvb_run_paged(const kvb_paged_args* a, double* ms) { return kvb_run_paged_steps(a, 1, ms); }
+
+int kvb_run_paged_split(const kvb_paged_args* a, double* decode_ms, double* reduce_ms) {
+    if (decode_ms) *decode_ms = 0.0;
+    if (reduce_ms) *reduce_ms = 0.0;
+    if (int st = validate_paged(a)) return st;
+    if (int st = ensure_device()) return st;
+    if (a->batch == 0) return KVB_OK;
+    float* part_out = nullptr;
+    float2* part_ml = nullptr;
+    if (int st = workspace_for(a, &part_out, &part_ml)) return st;
+    hipEvent_t e[3];
+    for (auto& x : e)
+        if (int st = get_event(&x)) return st;
+    KVB_HIP(hipEventRecord(e[0], g.stream));
+    if (int st = enqueue_paged(a, part_out, part_ml, e[1])) return st;
+    KVB_HIP(hipEventRecord(e[2], g.stream));
+    KVB_HIP(hipEventSynchronize(e[2]));
+    float d = 0.0f, r = 0.0f;
+    KVB_HIP(hipEventElapsedTime(&d, e[0], e[1]));
+    KVB_HIP(hipEventElapsedTime(&r, e[1], e[2]));
+    for (auto& x : e) g.spare.push_back(x);
+    if (decode_ms) *decode_ms = d;
+    if (reduce_ms) *reduce_ms = r;
+    return KVB_OK;
+}
+
+int kvb_check_naive(const kvb_naive_args* a) {
+    if (!a) return fail(KVB_EINVAL, "null arguments");
+    if (a->kv_type == KVB_KV_I8) return fail(KVB_EINVAL, "naive kernels take f32 or f16 caches");
+    if (a->kv_type != KVB_KV_F32 && a->kv_type != KVB_KV_F16) return fail(KVB_EINVAL, "unknown kv_type");
+    if (int st = check_shape(a->batch, a->num_heads, a->num_kv_heads, a->head_dim)) return st;
+    if (a->max_len < 0) return fail(KVB_EINVAL, "max_len < 0");
+    if (a->batch > 0 && !a->host_seq_lens) return fail(KVB_EINVAL, "host_seq_lens is required");
+    if (int st = check_lens(a->batch, a->host_seq_lens, a->max_len, (size_t)a->max_len)) return st;
+    if (a->batch > 0 && (!a->q || !a->seq_lens || !a->out || (a->max_len > 0 && (!a->k || !a->v))))
+        return fail(KVB_EINVAL, "null device pointer");
+    return KVB_OK;
+}
+
+int kvb_run_naive(const kvb_naive_args* a, double* ms) {
+    if (ms) *ms = 0.0;
+    if (int st = kvb_check_naive(a)) return st;
+    if (int st = ensure_device()) return st;
+    if (a->batch == 0) return KVB_OK;
+    const size_t need = (size_t)a->batch * a->num_heads * (size_t)std::max(a->max_len, 1) * sizeof(float);
+    if (int st = grow(&g.scores, &g.scores_bytes, need)) return st;
+    kvbk::NaiveParams p{a->q, a->k, a->v, a->seq_lens, static_cast<float*>(g.scores), a->out,
+                        a->num_heads, a->num_kv_heads, a->max_len, 1.0f / std::sqrt((float)a->head_dim)};
+    hipEvent_t e0, e1;
+    if (int st = get_event(&e0)) return st;
+    if (int st = get_event(&e1)) return st;
+    KVB_HIP(hipEventRecord(e0, g.stream));
+    const hipError_t e = kvbk::launch_naive(a->kv_type, a->head_dim, a->num_heads / a->num_kv_heads, p, a->batch, g.stream);
+    if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("naive launch: ") + hipGetErrorString(e));
+    KVB_HIP(hipEventRecord(e1, g.stream));
+    return finish(e0, e1, ms);
+}
+
+int kvb_begin_pipelined(void) {
+    if (int st = ensure_device()) return st;
+    g.pipelined = true;
+    g.timed.clear();
+    return KVB_OK;
+}
+
+size_t kvb_pipelined_pending(void) { return g.timed.size(); }
+
+int kvb_end_pipelined(double* ms, size_t cap, size_t* count) {
+    if (count) *count = 0;
+    if (int st = ensure_device()) return st;
+    g.pipelined = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> timed;
+    timed.swap(g.timed);
+    size_t i = 0;
+    int status = KVB_OK;
+    for (auto& [e0, e1] : timed) {
+        float f = 0.0f;
+        if (status == KVB_OK) {
+            hipError_t e = hipEventSynchronize(e1);
+            if (e == hipSuccess) e = hipEventElapsedTime(&f, e0, e1);
+            if (e != hipSuccess) status = fail(KVB_ERUNTIME, std::string("end_pipelined: ") + hipGetErrorString(e));
+        }
+        if (ms && i < cap) ms[i] = f;
+        ++i;
+        g.spare.push_back(e0);
+        g.spare.push_back(e1);
+    }
+    if (count) *count = i;
+    return status;
+}
+
+int kvb_run_read_bandwidth(const void* dev, size_t bytes, double* ms) {
+    if (ms) *ms = 0.0;
+    if (!dev || bytes == 0 || bytes % 16 != 0) return fail(KVB_EINVAL, "read probe needs a non-empty buffer of 16-byte words");
+    if (int st = ensure_device()) return st;
+    if (!g.sink) KVB_HIP(hipMalloc(&g.sink, kSinkFloats * sizeof(float)));
+    hipEvent_t e0, e1;
+    if (int st = get_event(&e0)) return st;
+    if (int st = get_event(&e1)) return st;
+    KVB_HIP(hipEventRecord(e0, g.stream));
+    const hipError_t e = kvbk::launch_read_bw(dev, bytes / 16, g.sink, g.stream);
+    if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("read_bw launch: ") + hipGetErrorString(e));
+    KVB_HIP(hipEventRecord(e1, g.stream));
+    return finish(e0, e1, ms);
+}
+
+int kvb_flush_gpu_caches(void) {
+    if (int st = ensure_device()) return st;
+    if (!g.flush_buf) KVB_HIP(hipMalloc(&g.flush_buf, kFlushBytes));
+    const hipError_t e = kvbk::launch_fill(g.flush_buf, kFlushBytes / 16, ++g.flush_value, g.stream);
+    if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("flush launch: ") + hipGetErrorString(e));
+    return KVB_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,145 @@
+"""The host layer (libkvb_host.so: generator, layout, scatter, int8 quantiser, poison) against the
+oracle bit for bit, and the C ABI's refusals, which happen before any GPU work (no GPU needed)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+
+def test_layout_equals_oracle(kvb, oracle):
+    lens = [0, 1, 63, 64, 65, 2047, 2048, 2049, 300]
+    w = kvb.Workload(kvb.Shape(1, 4, 2, 64), "f32", lens, seed=1)
+    for page in (1, 3, 16, 64, 128):
+        for pool in (1.0, 1.25, 1.5, 2.0, 3.0):
+            for seed in (0, 5, 2 ** 63 + 11):
+                c = kvb.PagedCache(w, page, seed, pool_factor=pool, poison=False)
+                want = oracle.make_paged_layout(lens, page, seed, pool)
+                assert np.array_equal(c.table, want)
+                assert c.num_blocks == oracle.layout_dims(lens, page, pool)[2]
+
+
+@pytest.mark.parametrize("kv", ["f32", "f16", "i8"])
+def test_paged_cache_equals_oracle(kvb, oracle, kv):
+    lens = [37, 0, 70, 16]
+    w = kvb.Workload(kvb.Shape(1, 8, 2, 64), kv, lens, seed=3, varied=(kv == "i8"))
+    c = kvb.PagedCache(w, 16, 77, pool_factor=2.0, poison=False)
+    if kv == "i8":
+        for src, pool, sc in ((w.k, c.k, c.k_scale), (w.v, c.v, c.v_scale)):
+            op, osc = oracle.quantize(w.shape, 16, c.table, lens, w.max_len, src, c.num_blocks)
+            assert np.array_equal(op, pool) and np.array_equal(osc.view(np.uint32), sc.view(np.uint32))
+        kd, vd = c.dequantized(w)
+        assert np.array_equal(kd, oracle.dequantize(w.shape, 16, c.table, lens, w.max_len, c.k, c.k_scale))
+    else:
+        for src, pool in ((w.k, c.k), (w.v, c.v)):
+            assert np.array_equal(oracle.scatter(w.shape, 16, c.table, lens, w.max_len, src, c.num_blocks).view(np.uint8),
+                                  pool.view(np.uint8))
+
+
+def test_f16_workload_is_rne_of_f32(kvb):
+    w = kvb.Workload(kvb.Shape(1, 8, 2, 128), "f16", [300, 41], seed=9, keep_f32=True, dist="normal")
+    assert np.array_equal(w.k32.astype(np.float16).view(np.uint16), w.k.view(np.uint16))
+    assert np.array_equal(w.v32.astype(np.float16).view(np.uint16), w.v.view(np.uint16))
+
+
+def test_workload_deterministic_and_distributions(kvb):
+    a = kvb.Workload(kvb.Shape(1, 8, 2, 128), "f32", [1000, 5], seed=4, threads=1)
+    b = kvb.Workload(kvb.Shape(1, 8, 2, 128), "f32", [1000, 5], seed=4, threads=7)
+    assert np.array_equal(a.k, b.k) and np.array_equal(a.v, b.v) and np.array_equal(a.q, b.q)
+    assert np.abs(a.k).max() < 1 and abs(a.k[0].mean()) < 0.01 and not a.k[1, :, 5:].any()
+    n = kvb.Workload(kvb.Shape(1, 8, 2, 128), "f32", [4000], seed=4, q_amp=1.0, dist="normal")
+    live = n.k[0].ravel()
+    assert abs(live.mean()) < 0.01 and abs(live.std() - 1) < 0.01 and abs(n.q.std() - 1) < 0.1
+    assert 0 < np.abs(n.k - kvb.Workload(kvb.Shape(1, 8, 2, 128), "f32", [4000], seed=5, dist="normal").k).max()
+
+
+def test_poison_marks_every_unowned_element(kvb):
+    lens = [1, 16, 17, 100, 0]
+    for kv, bad in (("f32", np.isnan), ("f16", np.isnan), ("i8", lambda x: x == -128)):
+        w = kvb.Workload(kvb.Shape(1, 4, 2, 64), kv, lens, seed=2)
+        c = kvb.PagedCache(w, 16, 9, pool_factor=3.0, poison=True)
+        owned = np.zeros(c.k.shape[:3], bool)  # [block][kvh][row]
+        for b, ln in enumerate(lens):
+            for t in range(ln):
+                owned[c.table[b, t // 16], :, t % 16] = True
+        marked = bad(c.k).all(axis=-1)
+        assert np.array_equal(marked, ~owned), kv
+        if kv == "i8":
+            used = set(c.table[c.table >= 0].tolist())
+            for blk in range(c.num_blocks):
+                assert np.isnan(c.k_scale[blk]).all() == (blk not in used)
+
+
+def test_mi355x_partition_policy(kvb):
+    # c4 (B 4, 64/8 heads, 32k): 4 * 8 groups per partition -> 1024 groups at part 1024.
+    assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768) == 1024
+    assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768, min_groups=512) == 2048
+    assert kvb.mi355x_part_tokens(kvb.Shape(1, 32, 8, 128), 512) == 256
+    assert kvb.mi355x_part_tokens(kvb.Shape(16, 32, 8, 128), 8192) == 1024
+
+
+class TestRefusals:
+    """kvb_check_paged / kvb_run_paged refuse what the reference's run_paged refuses
+    (src/metal_attn.mm:72-73, 107-117, 199-201), with no GPU involved."""
+
+    def args(self, kvb, **kw):
+        a = kvb.PagedArgsC()
+        a.batch, a.num_heads, a.num_kv_heads, a.head_dim = 2, 8, 2, 128
+        a.kv_type, a.page_size, a.max_blocks, a.max_len, a.part_tokens, a.share_kv = kvb.KV_F32, 16, 2, 32, 16, 1
+        self.lens = np.array(kw.pop("lens", [32, 32]), np.int32)
+        a.host_seq_lens = self.lens.ctypes.data
+        for name in ("q", "k", "v", "block_table", "seq_lens", "out"):
+            setattr(a, name, 0x1000)
+        for k, v in kw.items():
+            setattr(a, k, v)
+        return a
+
+    def status(self, kvb, a):
+        return kvb.hip.kvb_check_paged(ctypes.byref(a))
+
+    def test_valid_passes(self, kvb):
+        assert self.status(kvb, self.args(kvb)) == kvb.KVB_OK
+        assert self.status(kvb, self.args(kvb, lens=[0, 0], max_len=0)) == kvb.KVB_OK
+
+    @pytest.mark.parametrize("kw", [dict(lens=[33, 33], max_len=64), dict(lens=[32, 33], max_len=64),
+                                    dict(lens=[33, 33]), dict(lens=[32, 32], max_len=31), dict(lens=[-1, 32]),
+                                    dict(max_len=-1), dict(page_size=0), dict(part_tokens=-1), dict(head_dim=96),
+                                    dict(num_heads=6, num_kv_heads=4), dict(kv_type=2), dict(kv_type=7),
+                                    dict(max_blocks=-1), dict(host_seq_lens=None), dict(q=None), dict(out=None),
+                                    dict(workspace=0x1000, workspace_bytes=16)])
+    def test_refused(self, kvb, kw):
+        a = self.args(kvb, **kw)
+        assert self.status(kvb, a) == kvb.KVB_EINVAL, kvb.hip.kvb_last_error()
+        ms = ctypes.c_double(-1)
+        assert kvb.hip.kvb_run_paged(ctypes.byref(a), ctypes.byref(ms)) == kvb.KVB_EINVAL
+        assert ms.value == 0.0
+
+    def test_capacity_message_names_the_sequence(self, kvb):
+        self.status(kvb, self.args(kvb, lens=[32, 33], max_len=64))
+        assert b"sequence 1 has length 33" in kvb.hip.kvb_last_error()
+
+    def test_naive_refuses_int8_and_long(self, kvb):
+        a = kvb.NaiveArgsC()
+        a.batch, a.num_heads, a.num_kv_heads, a.head_dim, a.kv_type, a.max_len = 2, 8, 2, 128, kvb.KV_F32, 32
+        lens = np.array([32, 33], np.int32)
+        a.host_seq_lens = lens.ctypes.data
+        for name in ("q", "k", "v", "seq_lens", "out"):
+            setattr(a, name, 0x1000)
+        assert kvb.hip.kvb_check_naive(ctypes.byref(a)) == kvb.KVB_EINVAL
+        lens[1] = 32
+        assert kvb.hip.kvb_check_naive(ctypes.byref(a)) == kvb.KVB_OK
+        a.kv_type = kvb.KV_I8
+        assert kvb.hip.kvb_check_naive(ctypes.byref(a)) == kvb.KVB_EINVAL
+
+    def test_valid_without_gpu_is_no_device(self, kvb):
+        if kvb.gpu_available():
+            pytest.skip("a GPU is present")
+        ms = ctypes.c_double()
+        assert kvb.hip.kvb_run_paged(ctypes.byref(self.args(kvb)), ctypes.byref(ms)) == kvb.KVB_ENODEV
+
+    def test_workspace_size(self, kvb):
+        a = self.args(kvb, part_tokens=0, max_len=32)
+        # auto part for B 2, Hkv 2, 32 tokens is 64 -> one partition; slots 2*8*1
+        assert kvb.hip.kvb_paged_max_parts(ctypes.byref(a)) == 1
+        assert kvb.hip.kvb_paged_workspace_bytes(ctypes.byref(a)) == 16 * (128 * 4 + 8)
+        a.part_tokens = 5
+        assert kvb.hip.kvb_paged_max_parts(ctypes.byref(a)) == 7
