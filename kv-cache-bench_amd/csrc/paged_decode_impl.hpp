@@ -5,29 +5,32 @@
 // partition's normalised output o / l plus (m, l) to slot (b*H + h)*max_parts + part of the
 // split-K workspace. The mapping onto CDNA4 is this build's own:
 //
-//  * Each wave64 walks 16-token tiles of the partition (wave w takes tiles w, w+4, ...) and keeps
-//    its own online-softmax state (m, l, acc) for the QG heads; the workgroup merges the four
-//    wave states at the end, as the reference merges its simdgroups.
-//  * Scores S = Q K^T of a tile come from MFMA: one 16x16 tile with the 16 tokens as columns and
-//    the QG heads as rows. fp16/int8 caches use v_mfma_f32_16x16x32_f16 with q split into a high
-//    and a low fp16 part (rows 2h and 2h+1), so the product keeps ~22 bits of q and the fp32
-//    accumulation of the MFMA: K is read as stored, q is never rounded to fp16 as a whole. fp32
-//    caches use v_mfma_f32_16x16x4_f32 on q and K as they are (rows 2h+1 are zero).
-//  * K is loaded straight into the MFMA B-operand layout: lane l reads 16 bytes of token l%16,
-//    lanes l, l+16, l+32, l+48 cover 64 contiguous bytes of that row per instruction. The
-//    contraction order over d is free, so each storage type picks the d order its loads give and
-//    q is laid out to match (dslot_*).
-//  * The tile max is a 16-lane DPP row reduction; p = exp2(s - m) with q pre-scaled by
-//    scale*log2(e); p and the rescale factors go through LDS to the lanes that hold V.
-//  * V is read row-major (16 lanes x 16 bytes per fp16 row) and P*V runs on the VALU in fp32
-//    (a decode step has one query per head, so P*V is QG dot products per V element).
-//  * int8: bytes become exact fp16 (x ^ 0x80 under a 0x64 exponent, minus 1152) for the MFMA; the
-//    per-(block, KV head) K scale multiplies the score and the V scale multiplies p before P*V.
+//  * Each wave64 walks 32-token tiles of the partition (wave w takes tiles w, w+4, ...), with the
+//    next tile's K and V loads in flight while it computes one, and keeps its own online-softmax
+//    state; the workgroup merges the four wave states at the end, as the reference merges its
+//    simdgroups.
+//  * Both products run on MFMA. Scores come out transposed, S^T = K Q^T, one 16x16 tile per 16
+//    tokens: the tokens are rows, the 16 columns are the QG heads split into a high and a low fp16
+//    part (columns 2h, 2h+1), so K is read as stored and q keeps ~22 bits; the MFMA accumulates in
+//    fp32. fp32 caches use v_mfma_f32_16x16x4_f32 on q and K as they are (columns 2h+1 are zero).
+//  * In that layout a lane holds 8 tokens of one column, which is exactly its share of the P^T
+//    operand of O^T = V^T P^T (v_mfma_f32_16x16x32_f16 over 32 tokens): p = exp2(s - m) never
+//    leaves the lane, split into high and low fp16 parts like q. V^T comes from LDS, where the
+//    wave stores the V tile row-major with a 16-byte-chunk XOR swizzle that keeps the transposed
+//    2-byte reads free of bank conflicts. int8 V is widened to exact fp16 on the way into LDS.
+//  * K is loaded straight into the A-operand layout: lane l reads 16 bytes of token l%16, lanes l,
+//    l+16, l+32, l+48 cover 64 contiguous bytes of that row per instruction. The contraction order
+//    over d is free, so each storage type picks the d order its loads give and q matches (dslot).
+//  * DPP quad swaps merge the high/low columns; lane shuffles reduce the tile max and the sums
+//    across the four row groups.
+//  * int8: K bytes become exact fp16 (x ^ 0x80 under a 0x64 exponent, minus 1152) for the MFMA; the
+//    per-(block, KV head) K scale multiplies the score and the V scale multiplies p (normalised by a
+//    power of two per partition so the fp16 split of p * v_scale stays out of the subnormal range).
 //  * Tokens past the partition end get weight 0 and never reach the arithmetic as data. With
-//    `FAST` (every tile inside one page) the block id and scales are one scalar read per tile and
-//    K/V come through a buffer resource sized to the tile's live rows, so rows past the end read as
-//    zeros without touching memory; otherwise every lane looks up its own token's block (any page
-//    size) and lanes past the end re-read the partition's first token and zero it.
+//    `FAST` (every 16-token half tile inside one page) the block id and scales are one scalar read
+//    per half tile and K/V come through a buffer resource sized to its live rows, so rows past the
+//    end read as zeros without touching memory; otherwise every lane looks up its own token's block
+//    (any page size) and lanes past the end re-read the partition's first token and zero it.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -40,9 +43,12 @@ namespace kvbk {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kNegBig = -1e30f;  // "minus infinity" that keeps exp2(kNegBig - m) == 0 and no inf - inf
 constexpr float kLn2 = 0.693147180559945309f;
+constexpr int kHalf = 16;          // tokens per MFMA row block
+constexpr int kTok = 2 * kHalf;    // tokens per wave step (the K of a 16x16x32 MFMA)
 
 // ---- cross-lane helpers -------------------------------------------------------------------------
 
@@ -50,25 +56,17 @@ template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
 }
-constexpr int kQuadSwap1 = 0xB1;     // quad_perm [1,0,3,2]
-constexpr int kQuadSwap2 = 0x4E;     // quad_perm [2,3,0,1]
-constexpr int kRowHalfMirror = 0x141;
-constexpr int kRowMirror = 0x140;
+constexpr int kQuadSwap1 = 0xB1;  // quad_perm [1,0,3,2]: lane l <-> l ^ 1
 
-// Max / sum over the 16 lanes of a DPP row; every lane of the row gets the result.
-__device__ __forceinline__ float row_max16(float x) {
-    x = fmaxf(x, dpp<kQuadSwap1>(x));
-    x = fmaxf(x, dpp<kQuadSwap2>(x));
-    x = fmaxf(x, dpp<kRowHalfMirror>(x));
-    x = fmaxf(x, dpp<kRowMirror>(x));
-    return x;
+// The max / sum of a value over lanes l, l^16, l^32, l^48, on every lane. (Not v_permlane16/32_swap:
+// with the same value in both operands this compiler folds the two results into one.)
+__device__ __forceinline__ float max_x16_x32(float x) {
+    x = fmaxf(x, __shfl_xor(x, 16));
+    return fmaxf(x, __shfl_xor(x, 32));
 }
-__device__ __forceinline__ float row_sum16(float x) {
-    x += dpp<kQuadSwap1>(x);
-    x += dpp<kQuadSwap2>(x);
-    x += dpp<kRowHalfMirror>(x);
-    x += dpp<kRowMirror>(x);
-    return x;
+__device__ __forceinline__ float sum_x16_x32(float x) {
+    x += __shfl_xor(x, 16);
+    return x + __shfl_xor(x, 32);
 }
 __device__ __forceinline__ float wave_max(float x) {
     for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
@@ -93,48 +91,51 @@ __device__ __forceinline__ half8_t i8x8_to_half8(uint32_t w0, uint32_t w1) {
     return r;
 }
 
-// ---- per storage type: load widths and the d order of the MFMA contraction -------------------
+// ---- per storage type --------------------------------------------------------------------------
+// KLOADS: 16-byte K loads per lane per half tile; NJ: score MFMAs per half tile; kdoff/dslot: the d
+// order of the score contraction (a K load's first element, and MFMA j slot s). V is read row-major:
+// VL lanes per row (16 bytes each), 64/VL rows per load, NV loads per half tile. In LDS, V is fp16
+// (fp32 for fp32 caches) with row stride D elements; chunk ch of row t sits at ch ^ swz(t).
 
 template <int KIND, int D>
 struct KvT;
 
 template <int D>
 struct KvT<KV_F16, D> {
-    static constexpr int ESZ = 2;
-    static constexpr int KLOADS = D / 32;  // 16-byte loads per lane per tile for K
-    static constexpr int NJ = D / 32;      // 16x16x32 f16 MFMAs per tile
-    static constexpr int VDW = 4;          // dwords per lane per V row (8 elements)
-    // d of K byte-load c for row quad q4, and d of MFMA j slot s
+    static constexpr int ESZ = 2, KLOADS = D / 32, NJ = D / 32;
+    static constexpr int VL = D * 2 / 16, NV = kHalf * VL / 64;
+    static constexpr int LDS_ESZ = 2;
     __device__ static int kdoff(int c, int q4) { return 32 * c + 8 * q4; }
     __device__ static int dslot(int j, int q4, int s) { return 32 * j + 8 * q4 + s; }
+    __device__ static int swz(int t) { return 2 * ((t >> 2) & 3); }
 };
 template <int D>
 struct KvT<KV_I8, D> {
-    static constexpr int ESZ = 1;
-    static constexpr int KLOADS = D / 64;
-    static constexpr int NJ = D / 32;
-    static constexpr int VDW = 2;
+    static constexpr int ESZ = 1, KLOADS = D / 64, NJ = D / 32;
+    static constexpr int VL = D / 16, NV = kHalf * VL / 64;
+    static constexpr int LDS_ESZ = 2;
     __device__ static int kdoff(int c, int q4) { return 64 * c + 16 * q4; }
     __device__ static int dslot(int j, int q4, int s) { return 64 * (j >> 1) + 16 * q4 + 8 * (j & 1) + s; }
+    __device__ static int swz(int t) { return 2 * ((t >> 2) & 3); }
 };
 template <int D>
 struct KvT<KV_F32, D> {
-    static constexpr int ESZ = 4;
-    static constexpr int KLOADS = D / 16;
-    static constexpr int NJ = D / 4;       // 16x16x4 f32 MFMAs per tile
-    static constexpr int VDW = 8;
+    static constexpr int ESZ = 4, KLOADS = D / 16, NJ = D / 4;
+    static constexpr int VL = D * 4 / 16, NV = kHalf * VL / 64;
+    static constexpr int LDS_ESZ = 4;
     __device__ static int kdoff(int c, int q4) { return 16 * c + 4 * q4; }
     __device__ static int dslot(int j, int q4, int /*s*/) { return 16 * (j >> 2) + 4 * q4 + (j & 3); }
+    __device__ static int swz(int t) { return 4 * ((t >> 2) & 1); }
 };
 
-// Raw registers of one tile.
+// Raw registers of one 32-token tile.
 template <int KIND, int D>
 struct TileRegs {
     using T = KvT<KIND, D>;
-    static constexpr int LPR = D / 8, RPL = 64 / LPR, NV = kTile / RPL;
-    uint4 k[T::KLOADS];
-    uint32_t v[NV][T::VDW];
-    float kscale, vscale;  // int8: scales of this lane's K-layout token (p folds in the V scale)
+    uint4 k[2][T::KLOADS];
+    uint4 v[2][T::NV];
+    // int8: K and V scales of the tokens this lane holds in the score layout (FAST: one per half)
+    float ks[KIND == KV_I8 ? 8 : 1], vs[KIND == KV_I8 ? 8 : 1];
 };
 
 // ---- the kernel ---------------------------------------------------------------------------------
@@ -144,13 +145,17 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void paged_decode_kernel(DecodeP
     using T = KvT<KIND, D>;
     using R = TileRegs<KIND, D>;
     constexpr int W = kDecodeWaves;
-    constexpr int LPR = R::LPR, RPL = R::RPL, NV = R::NV, NJ = T::NJ;
+    constexpr int NJ = T::NJ, VL = T::VL, NV = T::NV, NMB = D / 16;
+    constexpr bool F32 = KIND == KV_F32;
     static_assert(QG == 1 || QG == 2 || QG == 4 || QG == 8, "QG must be 1, 2, 4 or 8");
+    // double-buffer the tile registers unless that would not fit (fp32 caches)
+    constexpr bool DOUBLE = !F32;
 
-    __shared__ float s_p[W][kTile][QG];   // p of the current tile, [token][head]
-    __shared__ float s_corr[W][QG];       // rescale factor of the current tile
-    __shared__ float s_acc[W][QG][D];     // final per-wave accumulators
-    __shared__ float2 s_ml[W][QG];        // final per-wave (m, l)
+    // Per wave: the V tile (32 rows of D elements, swizzled); after the loop it holds the wave's
+    // final accumulators [QG][D] fp32 for the merge (QG * D * 4 <= 32 * D * LDS_ESZ bytes).
+    static_assert(QG * 4 <= kTok * T::LDS_ESZ, "merge buffer must fit in the V tile");
+    __shared__ __attribute__((aligned(16))) unsigned char s_v[W][kTok * D * T::LDS_ESZ];
+    __shared__ float2 s_ml[W][QG];
 
     const int part = blockIdx.x, b = blockIdx.z;
     const int h0 = blockIdx.y * QG;
@@ -163,27 +168,27 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void paged_decode_kernel(DecodeP
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n = lane & 15, q4 = lane >> 4;              // MFMA: token column / stack row, row quad
-    const int vr = lane / LPR, vc = lane % LPR;            // V: row within a load, 8-element chunk
+    const int c = lane & 15, q4 = lane >> 4;  // MFMA: column (stack row of q) / token row, row quad
     const int32_t* bt = p.block_table + (size_t)b * p.max_blocks;
     const char* kbase = static_cast<const char*>(p.k);
     const char* vbase = static_cast<const char*>(p.v);
+    unsigned char* vt = s_v[wave];
 
-    // ---- q as MFMA A operand: stack row m = lane % 16 holds head m/2, high (m even) or low part.
-    const int hh = n >> 1, hl = n & 1;
-    const bool qrow = hh < QG;
-    const float* qp = p.q + ((size_t)b * H + h0 + (qrow ? hh : 0)) * D;
+    // ---- q as the B operand of S^T = K Q^T: column c holds head c/2, high (c even) or low part.
+    const int hh = c >> 1, hl = c & 1;
+    const bool qcol = hh < QG;
+    const float* qp = p.q + ((size_t)b * H + h0 + (qcol ? hh : 0)) * D;
     float up = 1.0f;  // scores are MFMA results times `up` (a power of two)
-    half8_t aq16[KIND == KV_F32 ? 1 : NJ];
-    float aq32[KIND == KV_F32 ? NJ : 1];
-    if constexpr (KIND == KV_F32) {
-        for (int j = 0; j < NJ; ++j) aq32[j] = (qrow && hl == 0) ? qp[T::dslot(j, q4, 0)] * p.qscale : 0.0f;
+    half8_t aq16[F32 ? 1 : NJ];
+    float aq32[F32 ? NJ : 1];
+    if constexpr (F32) {
+        for (int j = 0; j < NJ; ++j) aq32[j] = (qcol && hl == 0) ? qp[T::dslot(j, q4, 0)] * p.qscale : 0.0f;
     } else {
         float qv[NJ][8];
         float amax = 0.0f;
         for (int j = 0; j < NJ; ++j)
             for (int s = 0; s < 8; ++s) {
-                qv[j][s] = qrow ? qp[T::dslot(j, q4, s)] * p.qscale : 0.0f;
+                qv[j][s] = qcol ? qp[T::dslot(j, q4, s)] * p.qscale : 0.0f;
                 amax = fmaxf(amax, fabsf(qv[j][s]));
             }
         amax = wave_max(amax);
@@ -203,193 +208,233 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void paged_decode_kernel(DecodeP
             }
     }
 
+    // ---- int8: p * v_scale is split into fp16 high and low parts for the P*V MFMA. Normalise it by
+    // a power of two 2^-ve (ve: the exponent of the largest V scale of the partition) so it stays in
+    // fp16's normal range however small the scales are; the accumulators are rescaled by 2^ve at the
+    // end (exact).
+    float vdown = 1.0f, vupf = 1.0f;
+    if constexpr (KIND == KV_I8) {
+        float vmx = 0.0f;
+        for (int i = t0 / P + lane; i <= (t1 - 1) / P; i += 64) vmx = fmaxf(vmx, p.v_scale[(size_t)bt[i] * Hkv + kvh]);
+        vmx = wave_max(vmx);
+        int ve = 0;
+        if (vmx > 0.0f) frexpf(vmx, &ve);  // vmx < 2^ve
+        vdown = ldexpf(1.0f, -ve);
+        vupf = ldexpf(1.0f, ve);
+    }
+
     // ---- tile loads (no branches around them, so the compiler can keep a tile in flight)
-    auto load_v_row = [&](uint32_t* dst, auto&& load16, auto&& load8, int off) {
-        if constexpr (T::VDW == 8) {
-            const uint4 a = load16(off), c = load16(off + 16);
-            dst[0] = a.x; dst[1] = a.y; dst[2] = a.z; dst[3] = a.w;
-            dst[4] = c.x; dst[5] = c.y; dst[6] = c.z; dst[7] = c.w;
-        } else if constexpr (T::VDW == 4) {
-            const uint4 a = load16(off);
-            dst[0] = a.x; dst[1] = a.y; dst[2] = a.z; dst[3] = a.w;
-        } else {
-            const uint2 a = load8(off);
-            dst[0] = a.x; dst[1] = a.y;
-        }
-    };
     auto load_tile = [&](R& r, int tt) {
-        if constexpr (FAST) {
-            // The tile [tt, tt+16) lies in one page: one block id, and a buffer resource that
-            // covers exactly the tile's live rows, so rows at or past t1 read as zeros.
-            // A tile at or past t1 (the prefetch after the last one) gets an empty range.
-            const int tc = min(tt, t1 - 1);
-            const int blk = bt[tc / P];
-            const size_t row0 = ((size_t)blk * Hkv + kvh) * P + (tc % P);
-            // (readfirstlane: the value is wave-uniform, and a descriptor must live in SGPRs)
-            const int nbytes = __builtin_amdgcn_readfirstlane(max(0, min(kTile, t1 - tt)) * D * T::ESZ);
-            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<char*>(kbase + row0 * D * T::ESZ), (short)0, nbytes, 0x00020000);
-            const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<char*>(vbase + row0 * D * T::ESZ), (short)0, nbytes, 0x00020000);
-            for (int c = 0; c < T::KLOADS; ++c)
-                r.k[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                       rk, (n * D + T::kdoff(c, q4)) * T::ESZ, 0, 0));
-            auto v16 = [&](int off) { return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0)); };
-            auto v8 = [&](int off) { return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0)); };
-            for (int i = 0; i < NV; ++i) load_v_row(r.v[i], v16, v8, ((i * RPL + vr) * D + 8 * vc) * T::ESZ);
-            if constexpr (KIND == KV_I8) {
-                r.kscale = p.k_scale[(size_t)blk * Hkv + kvh];
-                r.vscale = p.v_scale[(size_t)blk * Hkv + kvh];
-            }
-        } else {
-            // Any page size: each lane finds the block of its own token. Lanes past t1 read the
-            // partition's first token (always live) and zero what they got.
-            const int tk = tt + n;
-            const bool kval = tk < t1;
-            const int tks = kval ? tk : t0;
-            const int kblk = bt[tks / P];
-            const size_t krow = ((size_t)kblk * Hkv + kvh) * P + (tks % P);
-            const char* kb = kbase + krow * D * T::ESZ;
-            for (int c = 0; c < T::KLOADS; ++c) {
-                const uint4 x = *reinterpret_cast<const uint4*>(kb + T::kdoff(c, q4) * T::ESZ);
-                r.k[c] = kval ? x : make_uint4(0, 0, 0, 0);
-            }
-            if constexpr (KIND == KV_I8) {
-                r.kscale = p.k_scale[(size_t)kblk * Hkv + kvh];
-                r.vscale = p.v_scale[(size_t)kblk * Hkv + kvh];
-            }
-            for (int i = 0; i < NV; ++i) {
-                const int tv = tt + i * RPL + vr;
-                const bool vval = tv < t1;
-                const int tvs = vval ? tv : t0;
-                const size_t vrow = ((size_t)bt[tvs / P] * Hkv + kvh) * P + (tvs % P);
-                const char* src = vbase + vrow * D * T::ESZ;
-                auto v16 = [&](int off) {
-                    const uint4 x = *reinterpret_cast<const uint4*>(src + off);
-                    return vval ? x : make_uint4(0, 0, 0, 0);
-                };
-                auto v8 = [&](int off) {
-                    const uint2 x = *reinterpret_cast<const uint2*>(src + off);
-                    return vval ? x : make_uint2(0, 0);
-                };
-                load_v_row(r.v[i], v16, v8, 8 * vc * T::ESZ);
+        for (int h = 0; h < 2; ++h) {
+            const int th = tt + h * kHalf;  // first token of this half tile
+            if constexpr (FAST) {
+                // [th, th+16) lies in one page: one block id and a buffer resource over exactly its
+                // live rows; a half at or past t1 (the prefetch after the last tile) gets an empty one.
+                const int tc = min(th, t1 - 1);
+                const int blk = bt[tc / P];
+                const size_t row0 = ((size_t)blk * Hkv + kvh) * P + (tc % P);
+                // (readfirstlane between the min and the max: the value is wave-uniform, and fused
+                // into one v_med3 it would land in a VGPR the prefetch may be writing)
+                const int rows = max(0, __builtin_amdgcn_readfirstlane(min(kHalf, t1 - th)));
+                const int nbytes = rows * D * T::ESZ;
+                const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<char*>(kbase + row0 * D * T::ESZ), (short)0, nbytes, 0x00020000);
+                const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<char*>(vbase + row0 * D * T::ESZ), (short)0, nbytes, 0x00020000);
+                for (int m = 0; m < T::KLOADS; ++m)
+                    r.k[h][m] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                              rk, (c * D + T::kdoff(m, q4)) * T::ESZ, 0, 0));
+                for (int i = 0; i < NV; ++i)
+                    r.v[h][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                              rv, (i * (64 / VL) + lane / VL) * D * T::ESZ + (lane % VL) * 16, 0, 0));
+                if constexpr (KIND == KV_I8) {
+                    r.ks[h] = p.k_scale[(size_t)blk * Hkv + kvh];
+                    r.vs[h] = p.v_scale[(size_t)blk * Hkv + kvh];
+                }
+            } else {
+                // Any page size: each lane finds the block of its own token. Lanes past t1 read the
+                // partition's first token (always live) and zero what they got.
+                const int tk = th + c;
+                const bool kval = tk < t1;
+                const int tks = kval ? tk : t0;
+                const size_t krow = ((size_t)bt[tks / P] * Hkv + kvh) * P + (tks % P);
+                const char* kb = kbase + krow * D * T::ESZ;
+                for (int m = 0; m < T::KLOADS; ++m) {
+                    const uint4 x = *reinterpret_cast<const uint4*>(kb + T::kdoff(m, q4) * T::ESZ);
+                    r.k[h][m] = kval ? x : make_uint4(0, 0, 0, 0);
+                }
+                for (int i = 0; i < NV; ++i) {
+                    const int tv = th + i * (64 / VL) + lane / VL;
+                    const bool vval = tv < t1;
+                    const int tvs = vval ? tv : t0;
+                    const size_t vrow = ((size_t)bt[tvs / P] * Hkv + kvh) * P + (tvs % P);
+                    const uint4 x = *reinterpret_cast<const uint4*>(vbase + vrow * D * T::ESZ + (lane % VL) * 16);
+                    r.v[h][i] = vval ? x : make_uint4(0, 0, 0, 0);
+                }
+                if constexpr (KIND == KV_I8) {
+                    for (int i = 0; i < 4; ++i) {  // the score-layout tokens th + 4*q4 + i of this lane
+                        const int ts = th + 4 * q4 + i;
+                        const int tss = ts < t1 ? ts : t0;
+                        const size_t slot = (size_t)bt[tss / P] * Hkv + kvh;
+                        r.ks[4 * h + i] = p.k_scale[slot];
+                        r.vs[4 * h + i] = p.v_scale[slot];
+                    }
+                }
             }
         }
     };
 
-    // ---- per-wave online-softmax state
-    // Lanes of row quad q4 own heads 2*q4 (a) and 2*q4+1 (b); m is uniform over the 16 lanes,
-    // l is a per-lane partial sum over that lane's tokens.
-    const int ha = 2 * q4, hb = 2 * q4 + 1;
-    float ma = kNegBig, mb = kNegBig, la = 0.0f, lb = 0.0f;
-    float acc[QG][8];
-    for (int h = 0; h < QG; ++h)
-        for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+    // ---- V tile -> LDS (row-major, swizzled 16-byte chunks; int8 widened to fp16)
+    auto store_v = [&](const R& r) {
+        for (int h = 0; h < 2; ++h)
+            for (int i = 0; i < NV; ++i) {
+                const int t = h * kHalf + i * (64 / VL) + lane / VL;  // tile row
+                const int ch = lane % VL;                             // 16-byte chunk of the loaded row
+                if constexpr (KIND == KV_I8) {
+                    const half8_t a = i8x8_to_half8(r.v[h][i].x, r.v[h][i].y);
+                    const half8_t bb = i8x8_to_half8(r.v[h][i].z, r.v[h][i].w);
+                    *reinterpret_cast<u32x4_t*>(vt + t * D * 2 + 16 * ((2 * ch) ^ T::swz(t))) = __builtin_bit_cast(u32x4_t, a);
+                    *reinterpret_cast<u32x4_t*>(vt + t * D * 2 + 16 * ((2 * ch + 1) ^ T::swz(t))) = __builtin_bit_cast(u32x4_t, bb);
+                } else {
+                    *reinterpret_cast<u32x4_t*>(vt + t * D * T::LDS_ESZ + 16 * (ch ^ T::swz(t))) = __builtin_bit_cast(u32x4_t, r.v[h][i]);
+                }
+            }
+    };
+
+    // ---- per-wave online-softmax state. Lane (c, q4) holds column c (head c/2) for the tokens
+    // 16h + 4*q4 + i of each tile (slot j = 4h + i of the P^T operand): m is uniform over the 8
+    // lanes of a head, l is the lane's partial sum over its tokens.
+    float m = kNegBig, l = 0.0f;
+    floatx4_t acc[NMB];
+    for (int mb = 0; mb < NMB; ++mb) acc[mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     auto compute_tile = [&](const R& r, int tt) {
-        // S = Q K^T for the 16 tokens of the tile
-        floatx4_t S = {0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (KIND == KV_F32) {
-            for (int j = 0; j < NJ; ++j) {
-                const uint4 w4 = r.k[j >> 2];
-                const uint32_t w = (j & 3) == 0 ? w4.x : (j & 3) == 1 ? w4.y : (j & 3) == 2 ? w4.z : w4.w;
-                S = __builtin_amdgcn_mfma_f32_16x16x4f32(aq32[j], __builtin_bit_cast(float, w), S, 0, 0, 0);
+        store_v(r);
+        // S^T = K Q^T for both halves
+        floatx4_t S[2];
+        for (int h = 0; h < 2; ++h) {
+            S[h] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (F32) {
+                for (int j = 0; j < NJ; ++j) {
+                    const uint4 w4 = r.k[h][j >> 2];
+                    const uint32_t w = (j & 3) == 0 ? w4.x : (j & 3) == 1 ? w4.y : (j & 3) == 2 ? w4.z : w4.w;
+                    S[h] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, w), aq32[j], S[h], 0, 0, 0);
+                }
+            } else if constexpr (KIND == KV_F16) {
+                for (int j = 0; j < NJ; ++j)
+                    S[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, r.k[h][j]), aq16[j], S[h], 0, 0, 0);
+            } else {
+                for (int j = 0; j < NJ; ++j) {
+                    const uint4 w4 = r.k[h][j >> 1];
+                    const half8_t kb = (j & 1) ? i8x8_to_half8(w4.z, w4.w) : i8x8_to_half8(w4.x, w4.y);
+                    S[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb, aq16[j], S[h], 0, 0, 0);
+                }
             }
-        } else if constexpr (KIND == KV_F16) {
-            for (int j = 0; j < NJ; ++j)
-                S = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq16[j], __builtin_bit_cast(half8_t, r.k[j]), S, 0, 0, 0);
-        } else {
-            for (int j = 0; j < NJ; ++j) {
-                const uint4 w4 = r.k[j >> 1];
-                const half8_t kb = (j & 1) ? i8x8_to_half8(w4.z, w4.w) : i8x8_to_half8(w4.x, w4.y);
-                S = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq16[j], kb, S, 0, 0, 0);
+        }
+        // scores of this lane's 8 tokens for head c/2: high + low columns, scaled, masked
+        float s[8];
+        bool valid[8];
+        float mx = kNegBig;
+        for (int h = 0; h < 2; ++h)
+            for (int i = 0; i < 4; ++i) {
+                const int j = 4 * h + i;
+                float f = up;
+                if constexpr (KIND == KV_I8) f *= FAST ? r.ks[h] : r.ks[j];
+                const float raw = S[h][i] + dpp<kQuadSwap1>(S[h][i]);
+                valid[j] = tt + h * kHalf + 4 * q4 + i < t1;
+                s[j] = valid[j] ? raw * f : kNegBig;
+                mx = fmaxf(mx, s[j]);
+            }
+        mx = max_x16_x32(mx);
+        const float mn = fmaxf(m, mx);
+        const float corr = __builtin_amdgcn_exp2f(m - mn);
+        m = mn;
+        float psum = 0.0f;
+        half8_t pb16;
+        float pb32[F32 ? 8 : 1];
+        for (int j = 0; j < 8; ++j) {
+            const float pr = valid[j] ? __builtin_amdgcn_exp2f(s[j] - mn) : 0.0f;
+            psum += pr;
+            float pv = pr;
+            if constexpr (KIND == KV_I8) pv *= (FAST ? r.vs[j >> 2] : r.vs[j]) * vdown;
+            if constexpr (F32) {
+                pb32[j] = hl ? 0.0f : pv;
+            } else {
+                const _Float16 hi = (_Float16)pv;
+                pb16[j] = hl ? (_Float16)(pv - (float)hi) : hi;
             }
         }
-        float f = up;
-        if constexpr (KIND == KV_I8) f *= r.kscale;
-        const bool valid = tt + n < t1;
-        const float sa = valid ? (S[0] + S[1]) * f : kNegBig;
-        const float sb = valid ? (S[2] + S[3]) * f : kNegBig;
-        const float mna = fmaxf(ma, row_max16(sa));
-        const float mnb = fmaxf(mb, row_max16(sb));
-        const float ca = __builtin_amdgcn_exp2f(ma - mna);
-        const float cb = __builtin_amdgcn_exp2f(mb - mnb);
-        const float pa = valid ? __builtin_amdgcn_exp2f(sa - mna) : 0.0f;
-        const float pb = valid ? __builtin_amdgcn_exp2f(sb - mnb) : 0.0f;
-        la = la * ca + pa;
-        lb = lb * cb + pb;
-        ma = mna;
-        mb = mnb;
-        float pv_scale = 1.0f;
-        if constexpr (KIND == KV_I8) pv_scale = r.vscale;
-        if (ha < QG) {
-            s_p[wave][n][ha] = pa * pv_scale;
-            if (n == 0) s_corr[wave][ha] = ca;
-        }
-        if (hb < QG) {
-            s_p[wave][n][hb] = pb * pv_scale;
-            if (n == 0) s_corr[wave][hb] = cb;
-        }
-        // LDS ops of one wave execute in order; the fence keeps the compiler from moving the
-        // reads above the writes.
+        l = l * corr + psum;
+        // corr is 1 for every head whose running max did not grow: skip the no-op rescale (the
+        // accumulators may live in AGPRs, where a multiply costs two moves as well)
+        if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0)
+            for (int mb = 0; mb < NMB; ++mb) acc[mb] *= corr;
+        // LDS ops of one wave execute in order; the fence keeps the compiler from moving the V^T
+        // reads above the stores.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        float corr[QG];
-        for (int h = 0; h < QG; ++h) corr[h] = s_corr[wave][h];
-        for (int h = 0; h < QG; ++h)
-            for (int e = 0; e < 8; ++e) acc[h][e] *= corr[h];
-        for (int i = 0; i < NV; ++i) {
-            float pr[QG];
-            for (int h = 0; h < QG; ++h) pr[h] = s_p[wave][i * RPL + vr][h];
-            float x[8];
-            if constexpr (KIND == KV_F32) {
-                for (int e = 0; e < 8; ++e) x[e] = __builtin_bit_cast(float, r.v[i][e]);
-            } else if constexpr (KIND == KV_F16) {
-                for (int e = 0; e < 4; ++e) {
-                    const half2_t h2 = __builtin_bit_cast(half2_t, r.v[i][e]);
-                    x[2 * e] = (float)h2[0];
-                    x[2 * e + 1] = (float)h2[1];
+        // O^T += V^T P^T, 16 rows of d per MFMA
+        for (int mb = 0; mb < NMB; ++mb) {
+            const int d = 16 * mb + c;
+            if constexpr (F32) {
+                for (int u = 0; u < 8; ++u) {
+                    const int t = 16 * (u >> 2) + 4 * q4 + (u & 3);
+                    const float a = *reinterpret_cast<const float*>(vt + t * D * 4 + 16 * ((d >> 2) ^ T::swz(t)) + 4 * (d & 3));
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, pb32[u], acc[mb], 0, 0, 0);
                 }
             } else {
-                for (int e = 0; e < 8; ++e) x[e] = (float)(int8_t)(r.v[i][e >> 2] >> (8 * (e & 3)));
+                half8_t a;
+                for (int j = 0; j < 8; ++j) {
+                    const int t = 16 * (j >> 2) + 4 * q4 + (j & 3);
+                    a[j] = *reinterpret_cast<const _Float16*>(vt + t * D * 2 + 16 * ((d >> 3) ^ T::swz(t)) + 2 * (d & 7));
+                }
+                acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb16, acc[mb], 0, 0, 0);
             }
-            for (int h = 0; h < QG; ++h)
-                for (int e = 0; e < 8; ++e) acc[h][e] = __builtin_fmaf(pr[h], x[e], acc[h][e]);
         }
+        // the next store_v overwrites the tile: keep it after these reads
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    // ---- walk the tiles: two register sets, the next tile's loads in flight while one computes.
-    // The prefetch is unconditional (past the end it reads zeros) so no branch splits the load
-    // counters the compiler tracks.
-    const int ntiles = (t1 - t0 + kTile - 1) / kTile;
-    R ra, rb;
+    // ---- walk the tiles. The prefetch is unconditional (past the end it reads zeros) so no
+    // branch splits the load counters the compiler tracks.
+    const int ntiles = (t1 - t0 + kTok - 1) / kTok;
     int it = wave;
-    load_tile(ra, t0 + it * kTile);
-    while (it < ntiles) {
-        load_tile(rb, t0 + (it + W) * kTile);
-        compute_tile(ra, t0 + it * kTile);
-        it += W;
-        if (it >= ntiles) break;
-        load_tile(ra, t0 + (it + W) * kTile);
-        compute_tile(rb, t0 + it * kTile);
-        it += W;
+    if constexpr (DOUBLE) {
+        R ra, rb;
+        load_tile(ra, t0 + it * kTok);
+        // (sched_barrier: the scheduler would otherwise sink part of the prefetch below the wait
+        // for the tile being computed, leaving less in flight)
+        while (it < ntiles) {
+            load_tile(rb, t0 + (it + W) * kTok);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_tile(ra, t0 + it * kTok);
+            it += W;
+            if (it >= ntiles) break;
+            load_tile(ra, t0 + (it + W) * kTok);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_tile(rb, t0 + it * kTok);
+            it += W;
+        }
+    } else {
+        R ra;
+        for (; it < ntiles; it += W) {
+            load_tile(ra, t0 + it * kTok);
+            compute_tile(ra, t0 + it * kTok);
+        }
     }
 
     // ---- merge: lanes -> wave state -> workgroup
-    la = row_sum16(la);
-    lb = row_sum16(lb);
-    for (int h = 0; h < QG; ++h)
-        for (int e = 0; e < 8; ++e)
-            for (int off = LPR; off < 64; off <<= 1) acc[h][e] += __shfl_xor(acc[h][e], off);
-    if (n == 0) {
-        if (ha < QG) s_ml[wave][ha] = make_float2(ma, la);
-        if (hb < QG) s_ml[wave][hb] = make_float2(mb, lb);
-    }
-    if (vr == 0)
-        for (int h = 0; h < QG; ++h)
-            for (int e = 0; e < 8; ++e) s_acc[wave][h][8 * vc + e] = acc[h][e];
+    l = sum_x16_x32(l);
+    float* sacc = reinterpret_cast<float*>(vt);  // reuse the wave's V tile: [QG][D]
+    for (int mb = 0; mb < NMB; ++mb)
+        for (int i = 0; i < 4; ++i) {
+            const float o = (acc[mb][i] + dpp<kQuadSwap1>(acc[mb][i])) * vupf;  // high + low columns
+            if (hl == 0 && qcol) sacc[hh * D + 16 * mb + 4 * q4 + i] = o;
+        }
+    if (hl == 0 && qcol && q4 == 0) s_ml[wave][hh] = make_float2(m, l);
     __syncthreads();
 
     for (int idx = threadIdx.x; idx < QG * D; idx += 64 * W) {
@@ -400,7 +445,7 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void paged_decode_kernel(DecodeP
         for (int w = 0; w < W; ++w) {
             const float wt = __builtin_amdgcn_exp2f(s_ml[w][h].x - M);
             L += s_ml[w][h].y * wt;
-            o += s_acc[w][h][d] * wt;
+            o += reinterpret_cast<const float*>(s_v[w])[h * D + d] * wt;
         }
         const size_t slot = ((size_t)b * H + h0 + h) * p.max_parts + part;
         p.part_out[slot * D + d] = o / L;
