@@ -71,7 +71,10 @@ hipError_t launch_paged_reduce(int head_dim, const ReduceParams& p, int batch, h
 // The naive three-pass baseline over a contiguous cache (f32 or f16).
 hipError_t launch_naive(int kind, int head_dim, int group, const NaiveParams& p, int batch, hipStream_t s);
 
-// Streaming read of n16 16-byte words; the guarded store into sink never fires for real data.
+// Streaming read of n16 16-byte words over kReadBwGroups workgroups; the guarded store into sink
+// (kReadBwSink floats) never fires for real data.
+constexpr int kReadBwGroups = 32768;
+constexpr size_t kReadBwSink = 2048 * 256;
 hipError_t launch_read_bw(const void* src, size_t n16, float* sink, hipStream_t s);
 // Overwrites n16 16-byte words with `value`.
 hipError_t launch_fill(void* dst, size_t n16, uint32_t value, hipStream_t s);

@@ -39,9 +39,8 @@ struct Runtime {
     size_t ws_bytes = 0;
     void* scores = nullptr;         // naive scores (grow-only)
     size_t scores_bytes = 0;
-    void* flush_buf = nullptr;      // cache-flush target
+    void* flush_buf = nullptr;      // cache-flush source
     float* sink = nullptr;          // read-probe sink
-    uint32_t flush_value = 0;
     bool pipelined = false;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> timed;
     std::vector<hipEvent_t> spare;
@@ -49,7 +48,7 @@ struct Runtime {
 Runtime g;
 
 constexpr size_t kFlushBytes = size_t(1) << 30;
-constexpr size_t kSinkFloats = 2048 * 256;
+constexpr size_t kSinkFloats = kvbk::kReadBwSink;
 
 int ensure_device() {
     if (g.ready) return KVB_OK;
@@ -429,10 +428,17 @@ int kvb_run_read_bandwidth(const void* dev, size_t bytes, double* ms) {
     return finish(e0, e1, ms);
 }
 
+// Reads (not writes) a 1 GiB buffer: that evicts the MALL and the L2s as well, and leaves no dirty
+// lines whose write-back would compete with the next timed run for HBM bandwidth.
 int kvb_flush_gpu_caches(void) {
     if (int st = ensure_device()) return st;
-    if (!g.flush_buf) KVB_HIP(hipMalloc(&g.flush_buf, kFlushBytes));
-    const hipError_t e = kvbk::launch_fill(g.flush_buf, kFlushBytes / 16, ++g.flush_value, g.stream);
+    if (!g.sink) KVB_HIP(hipMalloc(&g.sink, kSinkFloats * sizeof(float)));
+    if (!g.flush_buf) {
+        KVB_HIP(hipMalloc(&g.flush_buf, kFlushBytes));
+        const hipError_t e = kvbk::launch_fill(g.flush_buf, kFlushBytes / 16, 0x3f800000u, g.stream);
+        if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("flush fill: ") + hipGetErrorString(e));
+    }
+    const hipError_t e = kvbk::launch_read_bw(g.flush_buf, kFlushBytes / 16, g.sink, g.stream);
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("flush launch: ") + hipGetErrorString(e));
     return KVB_OK;
 }
