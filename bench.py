@@ -2,11 +2,11 @@
 on one MI355X, for BASELINE config c4 (fp16 cache, batch 4, 64 query / 8 KV heads, head_dim 128,
 32768-token contexts, page 128, partition 2048, 1.25x shuffled pool, N(0,1) data).
 
-A step is one decode step (paged_decode then paged_reduce) over inputs already resident in HBM,
-preceded by a 1 GiB cache flush outside its hipEvent pair (cold HBM, as the reference measures,
+A step is one decode step over inputs already resident in HBM: one launch of paged_decode with
+the partition merge fused in (the reference's paged_decode + paged_reduce), preceded by a 1 GiB
+read-only cache flush outside its hipEvent pair (cold HBM, as the reference measures,
 src/metal_attn.mm:266-276). value = algorithmic bytes (live K+V, q, out: src/workload.hpp:68-74) /
-median step time. The decode kernel's own event time over the same steps prices it against HBM
-peak (roofline). The reference's fp64 CPU path (oracle/_ref, else the C oracle) is timed on a
+median step time. The same event pairs time the kernel for the roofline (one launch per pair). The reference's fp64 CPU path (oracle/_ref, else the C oracle) is timed on a
 bounded sample of the same workload. Prints one JSON line.
 """
 from __future__ import annotations
@@ -31,18 +31,28 @@ def log(msg):
 
 
 def timed_steps(kvb, dev, part, steps, warmup):
-    """warmup + steps cold decode steps; returns per-step (decode_ms, reduce_ms) and the wall time."""
+    """warmup + steps cold decode steps (one fused paged_decode launch each, its hipEvent pair on the
+    library's stream); returns the per-step GPU ms and the wall time of the timed steps."""
     for _ in range(warmup):
         kvb.flush_gpu_caches()
-        dev.run_split(part)
+        dev.run(part)
     kvb.synchronize()
     t0 = time.perf_counter()
     times = []
     for _ in range(steps):
         kvb.flush_gpu_caches()
-        times.append(dev.run_split(part))
+        times.append(dev.run(part))
     kvb.synchronize()
     return times, time.perf_counter() - t0
+
+
+def split_steps(kvb, dev, part, steps):
+    """The reference's two-kernel form (paged_decode, then paged_reduce), timed per kernel."""
+    out = []
+    for _ in range(steps):
+        kvb.flush_gpu_caches()
+        out.append(dev.run_split(part))
+    return statistics.median(d for d, _ in out), statistics.median(r for _, r in out)
 
 
 def warm_chain(kvb, dev, part, steps=20):
@@ -109,18 +119,16 @@ def main():
     log(f"c4 ready in {time.perf_counter() - t_setup:.1f}s: {int(w.lens.sum())} tokens, pool {c.num_blocks} blocks")
 
     times, wall = timed_steps(kvb, dev, args.part, args.steps, args.warmup)
-    step_ms = [d + r for d, r in times]
-    med = statistics.median(step_ms)
-    decode_avg = statistics.mean(d for d, _ in times)
-    reduce_avg = statistics.mean(r for _, r in times)
+    med = statistics.median(times)
+    decode_avg = statistics.mean(times)  # the step is one launch of the fused paged_decode kernel
     bytes_step = w.min_bytes()
     value = bytes_step / (med * 1e-3) / 1e9
     s = w.shape
     kv_bytes = float(w.lens.sum()) * s.num_kv_heads * s.head_dim * 2 * 2
     decode_bytes = kv_bytes + s.batch * s.num_heads * s.head_dim * 4  # live K+V rows and q
     achieved = decode_bytes / (decode_avg * 1e-3) / 1e9
-    log(f"c4: step median {med * 1e3:.1f} us (decode {decode_avg * 1e3:.1f} us, reduce {reduce_avg * 1e3:.1f} us), "
-        f"{value:.0f} GB/s; wall {wall:.3f}s for {args.steps} steps")
+    log(f"c4: step median {med * 1e3:.1f} us (mean {decode_avg * 1e3:.1f} us), {value:.0f} GB/s; "
+        f"wall {wall:.3f}s for {args.steps} steps")
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
@@ -129,6 +137,9 @@ def main():
 
     extras = {}
     if not args.no_extras:
+        ud, ur = split_steps(kvb, dev, args.part, 10)
+        extras["unfused_decode_us"] = round(ud * 1e3, 2)
+        extras["unfused_reduce_us"] = round(ur * 1e3, 2)
         extras["warm_chain_us"] = round(warm_chain(kvb, dev, args.part) * 1e3, 2)
         extras["warm_gbps"] = round(bytes_step / (extras["warm_chain_us"] * 1e-6) / 1e9, 1)
         probe = kvb.Buffer(4 << 30)
@@ -144,7 +155,7 @@ def main():
         ci = kvb.PagedCache(wi, 128, 32768 * 131 + 128, pool_factor=1.25, poison=False)
         devi = kvb.DeviceCase(wi, ci)
         ti, _ = timed_steps(kvb, devi, args.part, args.steps, args.warmup)
-        medi = statistics.median(d + r for d, r in ti)
+        medi = statistics.median(ti)
         extras["int8_us_per_step"] = round(medi * 1e3, 2)
         extras["int8_gbps"] = round(wi.min_bytes() / (medi * 1e-3) / 1e9, 1)
         extras["int8_speedup_vs_fp16"] = round(med / medi, 3)

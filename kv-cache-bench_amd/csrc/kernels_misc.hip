@@ -8,7 +8,6 @@ namespace kvbk {
 namespace {
 
 constexpr float kNegBigR = -1e30f;
-constexpr float kLog2e = 1.4426950408889634f;
 
 // Merges the partitions of one (sequence, query head) (src/kernels.metal:123-147): weights
 // l_i * exp(m_i - M) over the ceil(len / part) written slots; an empty sequence gives exactly 0.
@@ -28,9 +27,9 @@ __global__ __launch_bounds__(D) void paged_reduce_kernel(ReduceParams p) {
     float L = 0.0f, acc = 0.0f;
     for (int i = 0; i < parts; ++i) {
         const float2 ml = p.part_ml[base + i];
-        const float w = ml.y * __builtin_amdgcn_exp2f((ml.x - M) * kLog2e);
+        const float w = partition_weight(ml.x, ml.y, M);
         L += w;
-        acc += w * p.part_out[(base + i) * D + d];
+        acc = __builtin_fmaf(w, p.part_out[(base + i) * D + d], acc);
     }
     o[d] = acc / L;
 }

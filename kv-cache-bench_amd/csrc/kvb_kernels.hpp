@@ -33,7 +33,29 @@ struct DecodeParams {
     int max_parts;
     int part_tokens;
     float qscale;               // softmax scale * log2(e): scores are kept in base-2 units
+    // Fused merge (null: leave the merge to paged_reduce). The last workgroup of a (sequence,
+    // head group) to finish merges its partitions into out; counters[b * (H / qg) + group] counts
+    // arrivals and is reset to 0 by that workgroup (it must start at 0). Requires
+    // qg * max_parts <= fused_merge_slots(kind, head_dim).
+    float* out;                 // [B][H][D]
+    int* counters;              // [B][H / qg]
 };
+
+// Weight of one partition in the merge, w = l exp(m - M) (m, M in natural-log units). paged_reduce
+// and the fused merge both use it, then sum L += w and o = fma(w, o_i, o) in partition order, so
+// the two give the same bits: w is rounded here, and the compiler may not fuse its product into
+// L's sum (which it would otherwise do in one kernel and not in the other).
+__device__ __forceinline__ float partition_weight(float m, float l, float M) {
+#pragma clang fp contract(off)
+    return l * __builtin_amdgcn_exp2f((m - M) * 1.4426950408889634f);
+}
+
+// Partition (m, l) pairs the fused merge stages in LDS (the V-tile space of one workgroup: 32
+// tokens x head_dim per wave, fp32 for f32 caches, fp16 otherwise). Past this the partitions are
+// merged by paged_reduce as a second kernel.
+constexpr int fused_merge_slots(int kind, int head_dim) {
+    return kDecodeWaves * 32 * head_dim * (kind == KV_F32 ? 4 : 2) / 8;
+}
 
 struct ReduceParams {
     const float* part_out;

@@ -26,6 +26,9 @@
 //  * int8: K bytes become exact fp16 (x ^ 0x80 under a 0x64 exponent, minus 1152) for the MFMA; the
 //    per-(block, KV head) K scale multiplies the score and the V scale multiplies p (normalised by a
 //    power of two per partition so the fp16 split of p * v_scale stays out of the subnormal range).
+//  * With DecodeParams::out set, the merge of the partitions (paged_reduce's job) is fused: the
+//    last workgroup of a (sequence, head group) to finish, found with an agent-scope counter,
+//    merges them, so a decode step is one kernel.
 //  * Tokens past the partition end get weight 0 and never reach the arithmetic as data. With
 //    `FAST` (every 16-token half tile inside one page) the block id and scales are one scalar read
 //    per half tile and K/V come through a buffer resource sized to its live rows, so rows past the
@@ -45,8 +48,11 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// Buffer-instruction cache policy sc1: device (agent) scope, coherent across the XCDs' L2s.
+constexpr int kScopeAgent = 16;
 constexpr float kNegBig = -1e30f;  // "minus infinity" that keeps exp2(kNegBig - m) == 0 and no inf - inf
 constexpr float kLn2 = 0.693147180559945309f;
+constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kHalf = 16;          // tokens per MFMA row block
 constexpr int kTok = 2 * kHalf;    // tokens per wave step (the K of a 16x16x32 MFMA)
 // Cache policy of the K/V loads: non-temporal (the data is read once per step). Measured on MI355X
@@ -143,8 +149,19 @@ struct TileRegs {
 
 // ---- the kernel ---------------------------------------------------------------------------------
 
+// Relaxed agent-scope accesses: on gfx950 these are global_store/global_load with sc1, coherent
+// across the XCDs' L2s for this one location without flushing the caches.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// (waves_per_eu(2): two waves per SIMD, 8 per CU, keep two tiles per wave in flight; the register
+// budget that leaves is 256 per lane)
 template <int KIND, int D, int QG, bool FAST>
-__global__ __launch_bounds__(64 * kDecodeWaves) void paged_decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(DecodeParams p) {
     using T = KvT<KIND, D>;
     using R = TileRegs<KIND, D>;
     constexpr int W = kDecodeWaves;
@@ -164,9 +181,14 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void paged_decode_kernel(DecodeP
     const int h0 = blockIdx.y * QG;
     const int len = p.seq_lens[b];
     const int t0 = part * p.part_tokens;
-    if (t0 >= len) return;  // uniform over the workgroup, before any barrier
-    const int t1 = min(len, t0 + p.part_tokens);
     const int H = p.num_heads, Hkv = p.num_kv_heads, P = p.page_size;
+    if (t0 >= len) {  // uniform over the workgroup, before any barrier
+        // fused merge: an empty sequence attends to nothing, its output is exactly 0
+        if (p.out && len == 0 && part == 0)
+            for (int idx = threadIdx.x; idx < QG * D; idx += 64 * W) p.out[((size_t)b * H + h0) * D + idx] = 0.0f;
+        return;
+    }
+    const int t1 = min(len, t0 + p.part_tokens);
     const int kvh = h0 / p.group;
 
     const int lane = threadIdx.x & 63;
@@ -451,9 +473,82 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void paged_decode_kernel(DecodeP
             o += reinterpret_cast<const float*>(s_v[w])[h * D + d] * wt;
         }
         const size_t slot = ((size_t)b * H + h0 + h) * p.max_parts + part;
-        p.part_out[slot * D + d] = o / L;
-        if (d == 0) p.part_ml[slot] = make_float2(M * kLn2, L);
+        // Agent-scope stores (sc1) write through this XCD's L2 to the device coherence point, where
+        // the merging workgroup, on whichever XCD, reads them.
+        store_agent(p.part_out + slot * D + d, o / L);
+        if (d == 0) {
+            store_agent(&p.part_ml[slot].x, M * kLn2);
+            store_agent(&p.part_ml[slot].y, L);
+        }
+        if (p.out && len <= p.part_tokens) p.out[((size_t)b * H + h0 + h) * D + d] = o / L;  // one partition
     }
+    if (!p.out || len <= p.part_tokens) return;
+
+    // ---- fused merge (src/kernels.metal:123-147): the last workgroup of this (sequence, head
+    // group) to arrive weighs the partitions by w_i = l_i exp(m_i - M), in paged_reduce's order
+    // (the two give identical bits). Message passing without whole-cache fences: each wave waits
+    // until its write-through partition stores are acknowledged (s_waitcnt vmcnt(0); __syncthreads
+    // alone does not wait for stores), the barrier orders that before thread 0's count (an
+    // agent-scope atomic), and the last workgroup issues its agent-scope (sc1) loads only after the
+    // count came back. An agent-scope release/acquire pair would instead write back and invalidate
+    // the whole L2 of the XCD in every workgroup (buffer_wbl2 / buffer_inv): 140 us per c4 step.
+    __shared__ int s_last;
+    const int nparts = (len + p.part_tokens - 1) / p.part_tokens;
+    int* counter = p.counters + (size_t)b * gridDim.y + blockIdx.y;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nparts - 1;
+    __syncthreads();
+    if (!s_last) return;
+
+    // (m_i, l_i) of the group's partitions into LDS (the V tiles are free again), all loads in flight
+    // at once; then w_i in place of l_i; then each thread sums 16-byte rows of part_out, eight
+    // partitions' loads in flight per batch. The merge is on the step's critical path: it starts
+    // when the last partition ends, so its latency, not its few bytes, is what costs.
+    static_assert(sizeof(s_v) / sizeof(float2) == fused_merge_slots(KIND, D), "merge staging size");
+    float2* s_pml = reinterpret_cast<float2*>(&s_v[0][0]);  // [QG][nparts]
+    const size_t gbase = ((size_t)b * H + h0) * p.max_parts;  // first slot of head h0
+    for (int e = threadIdx.x; e < QG * nparts; e += 64 * W) {
+        const size_t slot = gbase + (size_t)(e / nparts) * p.max_parts + e % nparts;
+        s_pml[e] = make_float2(load_agent(&p.part_ml[slot].x), load_agent(&p.part_ml[slot].y));
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < QG * nparts; e += 64 * W) {
+        const float2* row = s_pml + (e / nparts) * nparts;
+        float M = kNegBig;
+        for (int i = 0; i < nparts; ++i) M = fmaxf(M, row[i].x);
+        s_pml[e].y = partition_weight(s_pml[e].x, s_pml[e].y, M);
+    }
+    __syncthreads();
+    constexpr int kBatch = 8;
+    const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(
+        p.part_out + gbase * D, (short)0, QG * p.max_parts * D * 4, 0x00020000);
+    for (int e = threadIdx.x; e < QG * D / 4; e += 64 * W) {
+        const int h = e / (D / 4), d4 = e % (D / 4);
+        const float2* wrow = s_pml + h * nparts;
+        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float L = 0.0f;
+        for (int i0 = 0; i0 < nparts; i0 += kBatch) {
+            float4 v[kBatch];
+            for (int j = 0; j < kBatch; ++j)
+                if (i0 + j < nparts)
+                    v[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          rpo, ((h * p.max_parts + i0 + j) * D + 4 * d4) * 4, 0, kScopeAgent));
+            for (int j = 0; j < kBatch; ++j)
+                if (i0 + j < nparts) {
+                    const float wt = wrow[i0 + j].y;
+                    L += wt;
+                    o.x = __builtin_fmaf(wt, v[j].x, o.x);
+                    o.y = __builtin_fmaf(wt, v[j].y, o.y);
+                    o.z = __builtin_fmaf(wt, v[j].z, o.z);
+                    o.w = __builtin_fmaf(wt, v[j].w, o.w);
+                }
+        }
+        *reinterpret_cast<float4*>(p.out + ((size_t)b * H + h0 + h) * D + 4 * d4) =
+            make_float4(o.x / L, o.y / L, o.z / L, o.w / L);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int KIND, int D, int QG, bool FAST>

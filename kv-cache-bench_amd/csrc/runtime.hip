@@ -37,6 +37,8 @@ struct Runtime {
     hipStream_t stream = nullptr;
     void* ws = nullptr;             // split-K workspace (grow-only)
     size_t ws_bytes = 0;
+    void* counters = nullptr;       // fused-merge arrival counters (grow-only, kept at 0 between steps)
+    size_t counters_bytes = 0;
     void* scores = nullptr;         // naive scores (grow-only)
     size_t scores_bytes = 0;
     void* flush_buf = nullptr;      // cache-flush source
@@ -155,8 +157,20 @@ int query_heads_per_group(const kvb_paged_args* a) {
     return G % 8 == 0 ? 8 : G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
 }
 
-// Queues one decode step (paged_decode then paged_reduce); e_mid, if given, is recorded between.
-int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, hipEvent_t e_mid) {
+// Grows the fused-merge counters to B * H ints, zeroed (the kernel leaves them at 0).
+int counters_for(const kvb_paged_args* a, int** out) {
+    const size_t need = (size_t)a->batch * a->num_heads * sizeof(int);
+    if (g.counters_bytes < need || !g.counters) {
+        if (int st = grow(&g.counters, &g.counters_bytes, need)) return st;
+        KVB_HIP(hipMemsetAsync(g.counters, 0, g.counters_bytes, g.stream));
+    }
+    *out = static_cast<int*>(g.counters);
+    return KVB_OK;
+}
+
+// Queues one decode step. fused: one paged_decode that also merges the partitions; otherwise
+// paged_decode then paged_reduce, with e_mid (if given) recorded between them.
+int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, bool fused, hipEvent_t e_mid) {
     const int part = resolve_part(a);
     const int qg = query_heads_per_group(a);
     kvbk::DecodeParams p{};
@@ -177,6 +191,12 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, hip
     p.max_parts = max_parts_of(a);
     p.part_tokens = part;
     p.qscale = (1.0f / std::sqrt((float)a->head_dim)) * 1.4426950408889634f;
+    // fused merge when the group's partition (m, l) pairs fit its LDS staging
+    if (fused && qg * p.max_parts > kvbk::fused_merge_slots(a->kv_type, a->head_dim)) fused = false;
+    if (fused) {
+        p.out = a->out;
+        if (int st = counters_for(a, &p.counters)) return st;
+    }
     const bool fast = a->page_size % kvbk::kTile == 0 && part % kvbk::kTile == 0;
     hipError_t e = hipSuccess;
     switch (a->kv_type) {
@@ -185,6 +205,7 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, hip
         default: e = kvbk::launch_paged_decode_i8(a->head_dim, qg, fast, p, a->batch, g.stream); break;
     }
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("paged_decode launch: ") + hipGetErrorString(e));
+    if (fused) return KVB_OK;
     if (e_mid) KVB_HIP(hipEventRecord(e_mid, g.stream));
     kvbk::ReduceParams r{part_out, part_ml, a->seq_lens, a->out, a->num_heads, p.max_parts, part};
     e = kvbk::launch_paged_reduce(a->head_dim, r, a->batch, g.stream);
@@ -316,7 +337,7 @@ int kvb_run_paged_steps(const kvb_paged_args* a, int steps, double* ms) {
     if (int st = get_event(&e1)) return st;
     KVB_HIP(hipEventRecord(e0, g.stream));
     for (int i = 0; i < steps; ++i)
-        if (int st = enqueue_paged(a, part_out, part_ml, nullptr)) return st;
+        if (int st = enqueue_paged(a, part_out, part_ml, true, nullptr)) return st;
     KVB_HIP(hipEventRecord(e1, g.stream));
     return finish(e0, e1, ms);
 }
@@ -336,7 +357,7 @@ int kvb_run_paged_split(const kvb_paged_args* a, double* decode_ms, double* redu
     for (auto& x : e)
         if (int st = get_event(&x)) return st;
     KVB_HIP(hipEventRecord(e[0], g.stream));
-    if (int st = enqueue_paged(a, part_out, part_ml, e[1])) return st;
+    if (int st = enqueue_paged(a, part_out, part_ml, false, e[1])) return st;
     KVB_HIP(hipEventRecord(e[2], g.stream));
     KVB_HIP(hipEventSynchronize(e[2]));
     float d = 0.0f, r = 0.0f;

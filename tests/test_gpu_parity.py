@@ -222,6 +222,47 @@ def test_steps_pipelined_and_deterministic(gpu):
     dev.free()
 
 
+def test_fused_merge_reads_fresh_partitions(gpu):
+    """The fused merge reads partition results that other workgroups (other XCDs) wrote in the same
+    launch. Two cases alternate through the library's one workspace and counter array, so a merge
+    that saw a stale line would pick up the other case's partitions: every fused output must equal
+    the two-kernel (paged_decode, paged_reduce) output bit for bit, on every call."""
+    kvb = gpu
+    cases = []
+    for seed, lens in ((81, [8192, 5000, 3, 8192]), (82, [8192, 7777, 4096, 1])):
+        w = kvb.Workload(kvb.Shape(4, 64, 8, 128), "f16", lens, seed=seed)
+        c = kvb.PagedCache(w, 16, seed, pool_factor=1.25)
+        dev = kvb.DeviceCase(w, c)
+        dev.run_split(256)
+        cases.append((dev, dev.output()))
+    assert not np.array_equal(cases[0][1], cases[1][1])
+    for it in range(6):
+        for dev, want in cases:
+            dev.out.fill(0xFF)
+            dev.run(256)
+            assert np.array_equal(dev.output(), want), f"call {it}"
+    for dev, _ in cases:
+        dev.free()
+
+
+@pytest.mark.parametrize("kv,part", [("f16", 16), ("f16", 32), ("f32", 16)])
+def test_many_partitions(gpu, oracle, kv, part):
+    """Partition counts at and past what the fused merge stages in LDS (head group x partitions >
+    fused_merge_slots: the runtime then merges with paged_reduce as a second kernel)."""
+    kvb = gpu
+    w = kvb.Workload(kvb.Shape(2, 16, 2, 64), kv, [4096, 2049], seed=91)
+    c = kvb.PagedCache(w, 16, 91, pool_factor=1.25)
+    want, tol = expected(kvb, oracle, w, c)
+    dev = kvb.DeviceCase(w, c)
+    dev.out.fill(0xFF)
+    dev.run(part)
+    got = dev.output()
+    dev.run_split(part)
+    assert np.array_equal(got, dev.output())
+    dev.free()
+    assert oracle.max_abs_diff(got, want) <= tol
+
+
 def test_read_bandwidth_probe(gpu):
     kvb = gpu
     buf = kvb.Buffer(1 << 30)
