@@ -1,13 +1,15 @@
-"""Headline benchmark: effective KV-read GB/s and us per decode step of paged_decode -> paged_reduce
-on one MI355X, for BASELINE config c4 (fp16 cache, batch 4, 64 query / 8 KV heads, head_dim 128,
-32768-token contexts, page 128, partition 2048, 1.25x shuffled pool, N(0,1) data).
+"""Headline benchmark: effective KV-read GB/s and us per decode step of the paged decode path
+(the reference's paged_decode -> paged_reduce) on one MI355X. Default: BASELINE config c4 (fp16
+cache, batch 4, 64 query / 8 KV heads, head_dim 128, 32768-token contexts, page 128, partition
+chosen from the length by the MI355X policy (4096), 1.25x shuffled pool, N(0,1) data);
+--config c1|c2|c3|c5f16|c5i8 measures another BASELINE config with the same contract.
 
-A step is one decode step over inputs already resident in HBM: one launch of paged_decode with
-the partition merge fused in (the reference's paged_decode + paged_reduce), preceded by a 1 GiB
-read-only cache flush outside its hipEvent pair (cold HBM, as the reference measures,
-src/metal_attn.mm:266-276). value = algorithmic bytes (live K+V, q, out: src/workload.hpp:68-74) /
-median step time. The same event pairs time the kernel for the roofline (one launch per pair). The reference's fp64 CPU path (oracle/_ref, else the C oracle) is timed on a
-bounded sample of the same workload. Prints one JSON line.
+A step is one decode step over inputs already resident in HBM: one launch of paged_decode with the
+partition merge fused in, preceded by a 1 GiB read-only cache flush outside its hipEvent pair (cold
+HBM, as the reference measures, src/metal_attn.mm:266-276). value = algorithmic bytes (live K+V, q,
+out: src/workload.hpp:68-74) / median step time. The same event pairs time the kernel for the
+roofline (one launch per pair). The reference's fp64 CPU path (oracle/_ref, else the C oracle) is
+timed on a bounded sample of the same workload. Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -61,15 +63,20 @@ def warm_chain(kvb, dev, part, steps=20):
     return dev.run(part, steps=steps) / steps
 
 
-def cpu_baseline(oracle, w, seconds_budget=20.0):
+def cpu_baseline(kvb, oracle, w, c, seconds_budget=20.0):
     """The reference's fp64 attention (oracle/_ref when built, else this build's C oracle) on a bounded
-    sample of the workload: the first sequence (all its heads, full context)."""
-    import numpy as np
-
+    sample of the workload: the first non-empty sequence, all its heads, full context. int8 caches
+    are dequantised first (outside the timing), as the reference's PagedCache::reference does."""
     threads = max(1, min(16, os.cpu_count() or 1))
+    b = next(i for i, L in enumerate(w.lens) if L > 0)
     s1 = type(w.shape)(1, w.shape.num_heads, w.shape.num_kv_heads, w.shape.head_dim)
-    lens = w.lens[:1]
-    q, k, v = w.q[:1], w.k[:1], w.v[:1]
+    lens = w.lens[b:b + 1]
+    if w.kv_type == kvb.KV_I8:
+        kd, vd = c.dequantized(w)
+        k, v = kd[b:b + 1], vd[b:b + 1]
+    else:
+        k, v = w.k[b:b + 1], w.v[b:b + 1]
+    q = w.q[b:b + 1]
     use_ref = oracle.ref is not None
     fn = oracle.ref_attention if use_ref else oracle.attention
     fn(s1, lens, w.max_len, q, k, v, threads=threads)  # warm-up
@@ -80,18 +87,34 @@ def cpu_baseline(oracle, w, seconds_budget=20.0):
         fn(s1, lens, w.max_len, q, k, v, threads=threads)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    sample_bytes = float(lens.sum()) * w.shape.num_kv_heads * w.shape.head_dim * 2 * 2 + \
-        w.shape.num_heads * w.shape.head_dim * 2 * 4
+    esz = {kvb.KV_F32: 4, kvb.KV_F16: 2, kvb.KV_I8: 1}[w.kv_type]
+    sample_bytes = float(lens[0]) * w.shape.num_kv_heads * w.shape.head_dim * esz * 2 + \
+        w.shape.num_heads * w.shape.head_dim * 4 * 2
+    per_step = med * float(w.lens.sum()) / float(lens[0])
     return {
         "value": round(sample_bytes / med / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "reference" if use_ref else "port",
-        "sample": f"sequence 0 of {w.shape.batch} ({w.shape.num_heads} heads x {int(lens[0])} tokens, fp16 K/V), "
+        "sample": f"sequence {b} of {w.shape.batch} ({w.shape.num_heads} heads x {int(lens[0])} tokens), fp64 "
+                  f"attention on the stored {'dequantised int8' if w.kv_type == kvb.KV_I8 else 'K/V'} values, "
                   f"median of {len(times)} runs after 1 warm-up: {med * 1e3:.1f} ms "
-                  f"(~{med * w.shape.batch * 1e3:.0f} ms per full step)",
-        "ms_per_step_extrapolated": round(med * w.shape.batch * 1e3, 2),
+                  f"(~{per_step * 1e3:.0f} ms per full step by token count)",
+        "ms_per_step_extrapolated": round(per_step * 1e3, 2),
     }
+
+
+WORKLOAD_TEXT = {
+    "c1": "c1: fp32 paged decode, batch 1, 32 q / 8 KV heads (GQA 4), head_dim 128, context 512, page 16",
+    "c2": "c2: fp16 paged decode, batch 8, 32 q / 8 KV heads (GQA 4), head_dim 128, context 4096, page 16",
+    "c3": "c3: int8 paged decode (per-(page, KV head) scales), batch 16, 32 q / 8 KV heads, head_dim 128, "
+          "context 8192, page 64",
+    "c4": "c4: fp16 paged decode, batch 4, 64 q / 8 KV heads (GQA 8), head_dim 128, context 32768, page 128",
+    "c5f16": "c5: fp16 ragged batch of 72 (64 lengths ~U[1,16384] + 0,1,63,64,65,2047,2048,2049), 32 q / 8 KV "
+             "heads, head_dim 128, page 64",
+    "c5i8": "c5: int8 ragged batch of 72 (64 lengths ~U[1,16384] + 0,1,63,64,65,2047,2048,2049), 32 q / 8 KV "
+            "heads, head_dim 128, page 64",
+}
 
 
 def main():
@@ -99,9 +122,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--part", type=int, default=2048, help="partition tokens for c4 (BASELINE: >= 2048)")
+    ap.add_argument("--config", default="c4", choices=sorted(WORKLOAD_TEXT))
+    ap.add_argument("--part", type=int, default=None,
+                    help="partition tokens (default: the config's, else the MI355X policy; 0 = auto_part_tokens)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extras", action="store_true", help="skip the int8, warm and probe measurements")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the two-kernel, warm, probe and (c4) int8 measurements")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU would run the same kernel "
@@ -114,33 +140,36 @@ def main():
         sys.exit(1)
     log(f"device: {kvb.device_name()}")
     t_setup = time.perf_counter()
-    w, c, cfg = kvb.make_config("c4", threads=16)
+    w, c, cfg = kvb.make_config(args.config, threads=16)
+    part = kvb.config_part(cfg, w) if args.part is None else args.part
     dev = kvb.DeviceCase(w, c)
-    log(f"c4 ready in {time.perf_counter() - t_setup:.1f}s: {int(w.lens.sum())} tokens, pool {c.num_blocks} blocks")
+    nparts = dev.max_parts(part)
+    part_res = kvb.auto_part_tokens(w.shape.batch, w.shape.num_kv_heads, w.max_len) if part == 0 else part
+    log(f"{args.config} ready in {time.perf_counter() - t_setup:.1f}s: {int(w.lens.sum())} tokens, "
+        f"pool {c.num_blocks} blocks, partition {part_res} ({nparts} per sequence)")
 
-    times, wall = timed_steps(kvb, dev, args.part, args.steps, args.warmup)
+    times, wall = timed_steps(kvb, dev, part, args.steps, args.warmup)
     med = statistics.median(times)
-    decode_avg = statistics.mean(times)  # the step is one launch of the fused paged_decode kernel
+    kernel_avg = statistics.mean(times)  # the step is one launch of the fused paged_decode kernel
     bytes_step = w.min_bytes()
     value = bytes_step / (med * 1e-3) / 1e9
-    s = w.shape
-    kv_bytes = float(w.lens.sum()) * s.num_kv_heads * s.head_dim * 2 * 2
-    decode_bytes = kv_bytes + s.batch * s.num_heads * s.head_dim * 4  # live K+V rows and q
-    achieved = decode_bytes / (decode_avg * 1e-3) / 1e9
-    log(f"c4: step median {med * 1e3:.1f} us (mean {decode_avg * 1e3:.1f} us), {value:.0f} GB/s; "
+    achieved = bytes_step / (kernel_avg * 1e-3) / 1e9
+    log(f"{args.config}: step median {med * 1e3:.1f} us (mean {kernel_avg * 1e3:.1f} us), {value:.0f} GB/s; "
         f"wall {wall:.3f}s for {args.steps} steps")
 
     traffic = None
-    if os.path.exists(TRAFFIC_FILE):
+    if args.config == "c4" and os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("bytes_per_launch")
 
     extras = {}
+    if w.kv_type == kvb.KV_I8:
+        extras["scale_bytes"] = c.scale_bytes(w)  # read too, reported apart from value (src/workload.hpp:68-74)
     if not args.no_extras:
-        ud, ur = split_steps(kvb, dev, args.part, 10)
+        ud, ur = split_steps(kvb, dev, part, 10)
         extras["unfused_decode_us"] = round(ud * 1e3, 2)
         extras["unfused_reduce_us"] = round(ur * 1e3, 2)
-        extras["warm_chain_us"] = round(warm_chain(kvb, dev, args.part) * 1e3, 2)
+        extras["warm_chain_us"] = round(warm_chain(kvb, dev, part) * 1e3, 2)
         extras["warm_gbps"] = round(bytes_step / (extras["warm_chain_us"] * 1e-6) / 1e9, 1)
         probe = kvb.Buffer(4 << 30)
         probe.fill(1)
@@ -149,12 +178,17 @@ def main():
         extras["probe_gbps"] = round((4 << 30) / (statistics.median(pt) * 1e-3) / 1e9, 1)
         extras["pct_of_probe"] = round(100 * value / extras["probe_gbps"], 1)
         probe.free()
+    if not args.no_extras and args.config == "c4":
         # the same shape with an int8 cache (per-(page, KV head) scales): the int8 / fp16 speed ratio
         dev.free()
+        s = w.shape
         wi = kvb.Workload(s, "i8", list(w.lens), seed=32768, q_amp=1.0, dist="normal", threads=16)
         ci = kvb.PagedCache(wi, 128, 32768 * 131 + 128, pool_factor=1.25, poison=False)
         devi = kvb.DeviceCase(wi, ci)
-        ti, _ = timed_steps(kvb, devi, args.part, args.steps, args.warmup)
+        parti = kvb.mi355x_part_tokens(s, wi.max_len, min_groups=kvb.mi355x_min_groups(kvb.KV_I8)) \
+            if args.part is None else args.part
+        extras["int8_part"] = parti
+        ti, _ = timed_steps(kvb, devi, parti, args.steps, args.warmup)
         medi = statistics.median(ti)
         extras["int8_us_per_step"] = round(medi * 1e3, 2)
         extras["int8_gbps"] = round(wi.min_bytes() / (medi * 1e-3) / 1e9, 1)
@@ -166,9 +200,10 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(graft.load_oracle(), w)
+        cpu = cpu_baseline(kvb, graft.load_oracle(), w, c)
         log(f"cpu baseline: {cpu['sample']}, {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['kind']})")
 
+    storage = {kvb.KV_F32: "f32", kvb.KV_F16: "f16", kvb.KV_I8: "i8"}[w.kv_type]
     line = {
         "metric": "effective KV-read GB/s (% of HBM peak) + us per decode step, 1 MI355X",
         "value": round(value, 1),
@@ -182,15 +217,15 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 storage, f32 math",
-        "data": "synthetic: q, K, V ~ N(0,1), K/V rounded to fp16, shuffled block table over a 1.25x pool",
-        "config": {"workload": "c4: fp16 paged decode, batch 4, 64 q / 8 KV heads (GQA 8), head_dim 128, "
-                               "context 32768, page 128, partition %d, cold HBM (1 GiB flush per step)" % args.part,
-                   "bytes_per_step": bytes_step, "timed_wall_s": round(wall, 4)},
+        "dtype": "f32",
+        "data": "synthetic: q, K, V ~ N(0,1) from seeds, K/V stored as %s; shuffled block table over a %gx pool"
+                % ({"f32": "fp32", "f16": "fp16 (RNE)", "i8": "int8 per-(page, KV head) scales"}[storage], cfg["pool"]),
+        "config": {"workload": WORKLOAD_TEXT[args.config] + ", partition %d, cold HBM (1 GiB flush per step)" % part_res,
+                   "kv_storage": storage, "bytes_per_step": bytes_step, "timed_wall_s": round(wall, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "paged_decode", "kernel_avg_us": round(decode_avg * 1e3, 2),
-                     "bytes_per_launch": decode_bytes},
+                     "kernel": "paged_decode", "kernel_avg_us": round(kernel_avg * 1e3, 2),
+                     "bytes_per_launch": bytes_step},
         "cpu_baseline": cpu,
     }
     line.update(extras)

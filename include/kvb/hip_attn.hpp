@@ -66,10 +66,14 @@ inline int auto_part_tokens(const Shape& s, int max_len) {
 }
 
 // The MI355X partition policy: the largest power of two in [min_part, max_part] whose workgroup
-// count B * ceil(H / qg) * ceil(max_len / part) still reaches `min_groups` (by default 4 per CU of
-// a 256-CU MI355X); longer partitions mean fewer partial results to merge, more workgroups keep
-// more bytes in flight. qg is the number of query heads one workgroup serves.
-int mi355x_part_tokens(const Shape& s, int max_len, int min_groups = 1024, int min_part = 256, int max_part = 4096);
+// count B * ceil(H / qg) * ceil(max_len / part) still reaches `min_groups` (qg: the query heads one
+// workgroup serves). Longer partitions mean fewer partial results to merge and a shorter prologue
+// per token; enough workgroups keep enough bytes in flight. Measured on MI355X (c4): fp16 is
+// fastest at one workgroup per CU (min_groups 256, the default), int8, whose tiles carry half the
+// bytes for the same work, at two (mi355x_min_groups).
+int mi355x_part_tokens(const Shape& s, int max_len, int min_groups = 256, int min_part = 256, int max_part = 4096);
+// min_groups of the policy for a storage type: 512 for int8, 256 otherwise.
+inline int mi355x_min_groups(KvType t) { return t == KvType::i8 ? 512 : 256; }
 
 struct PagedArgs {
     Shape shape;

@@ -96,18 +96,21 @@ size_t kvb_paged_workspace_bytes(const kvb_paged_args* a);
  * sizes, needs no GPU. Lets a host layer refuse before it uploads anything. */
 int kvb_check_paged(const kvb_paged_args* a);
 
-/* One decode step: paged_decode then paged_reduce on one stream (run_paged, src/metal_attn.hpp:86).
- * *ms = GPU time from before the first kernel to after the last (hipEvent pair); 0 in pipelined
- * mode. Refuses (KVB_EINVAL, before any GPU work, output untouched) part_tokens < 0, max_len < 0,
+/* One decode step (run_paged, src/metal_attn.hpp:86): the reference's paged_decode + paged_reduce
+ * as one launch of paged_decode whose last workgroup per (sequence, KV-head group) merges the
+ * partitions; two kernels (paged_decode, then paged_reduce) when a group's partition count
+ * exceeds what that merge stages on chip (query heads per group x max_parts > 1024 for f16/i8 at
+ * head_dim 128, 512 at 64; twice that for f32). Either form gives the same bits. *ms = GPU time
+ * from before the first kernel to after the last (hipEvent pair); 0 in pipelined mode. Refuses (KVB_EINVAL, before any GPU work, output untouched) part_tokens < 0, max_len < 0,
  * page_size <= 0, I8 without scales, a length < 0 or > max_len or > max_blocks * page_size,
  * head_dim not 64/128, H % Hkv != 0 (src/metal_attn.mm:72-73, 107-117, 199-201). */
 int kvb_run_paged(const kvb_paged_args* a, double* ms);
 /* `steps` decode steps on the same inputs, back to back on one stream, one event pair around them
  * (run_paged_steps, src/metal_attn.hpp:91). */
 int kvb_run_paged_steps(const kvb_paged_args* a, int steps, double* ms);
-/* One synchronous decode step timed per kernel: *decode_ms and *reduce_ms are the hipEvent times
- * of paged_decode and of paged_reduce. Not in the reference (its timing is per command buffer,
- * src/metal_attn.mm:119-130); used to price the decode kernel against its roofline. */
+/* One synchronous decode step in the reference's two-kernel form, timed per kernel: *decode_ms and
+ * *reduce_ms are the hipEvent times of paged_decode (no merge) and of paged_reduce. Not in the
+ * reference (its timing is per command buffer, src/metal_attn.mm:119-130). */
 int kvb_run_paged_split(const kvb_paged_args* a, double* decode_ms, double* reduce_ms);
 
 /* ---- naive 3-pass baseline (NaiveArgs / run_naive, src/metal_attn.hpp:71-87) ------------- */

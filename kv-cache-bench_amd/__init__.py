@@ -148,9 +148,15 @@ def auto_part_tokens(batch, num_kv_heads, max_len) -> int:
     return hip.kvb_auto_part_tokens(batch, num_kv_heads, max_len)
 
 
-def mi355x_part_tokens(shape, max_len, min_groups=1024, min_part=256, max_part=4096) -> int:
+def mi355x_part_tokens(shape, max_len, min_groups=256, min_part=256, max_part=4096) -> int:
+    """The MI355X partition policy (kvb::mi355x_part_tokens, include/kvb/hip_attn.hpp)."""
     return host.kvbh_mi355x_part_tokens(shape.batch, shape.num_heads, shape.num_kv_heads, shape.head_dim, max_len,
                                         min_groups, min_part, max_part)
+
+
+def mi355x_min_groups(kv_type) -> int:
+    """The policy's workgroup target for a storage type: 512 for int8, 256 otherwise."""
+    return 512 if kv_type == KV_I8 else 256
 
 
 @dataclass
@@ -439,7 +445,8 @@ def softmax_scale(head_dim):
 
 
 # The BASELINE configurations (BASELINE.json "configs"): shape, dtype, lengths, page, partition
-# (0 = auto_part_tokens, "mi355x" = mi355x_part_tokens), pool factor; data N(0,1).
+# (a number where BASELINE names one, "mi355x" = mi355x_part_tokens where it leaves the choice to the
+# build, c4's "chosen from length"), pool factor; data N(0,1).
 C5_FORCED = (0, 1, 63, 64, 65, 2047, 2048, 2049)
 
 
@@ -452,11 +459,18 @@ def c5_lengths(seed=5):
 CONFIGS = {
     "c1": dict(shape=Shape(1, 32, 8, 128), kv="f32", lens=[512], page=16, part=128, pool=2.0),
     "c2": dict(shape=Shape(8, 32, 8, 128), kv="f16", lens=[4096] * 8, page=16, part=512, pool=1.5),
-    "c3": dict(shape=Shape(16, 32, 8, 128), kv="i8", lens=[8192] * 16, page=64, part=0, pool=1.0),
-    "c4": dict(shape=Shape(4, 64, 8, 128), kv="f16", lens=[32768] * 4, page=128, part=2048, pool=1.25),
-    "c5f16": dict(shape=Shape(72, 32, 8, 128), kv="f16", lens=None, page=64, part=0, pool=3.0),
-    "c5i8": dict(shape=Shape(72, 32, 8, 128), kv="i8", lens=None, page=64, part=0, pool=3.0),
+    "c3": dict(shape=Shape(16, 32, 8, 128), kv="i8", lens=[8192] * 16, page=64, part="mi355x", pool=1.0),
+    "c4": dict(shape=Shape(4, 64, 8, 128), kv="f16", lens=[32768] * 4, page=128, part="mi355x", pool=1.25),
+    "c5f16": dict(shape=Shape(72, 32, 8, 128), kv="f16", lens=None, page=64, part="mi355x", pool=3.0),
+    "c5i8": dict(shape=Shape(72, 32, 8, 128), kv="i8", lens=None, page=64, part="mi355x", pool=3.0),
 }
+
+
+def config_part(cfg, w) -> int:
+    """The partition tokens a configuration runs with (its own number, or the MI355X policy for w)."""
+    if cfg["part"] == "mi355x":
+        return mi355x_part_tokens(w.shape, w.max_len, min_groups=mi355x_min_groups(w.kv_type))
+    return cfg["part"]
 
 
 def make_config(name, seed=None, poison=False, threads=0):

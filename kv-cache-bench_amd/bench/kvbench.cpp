@@ -1,6 +1,6 @@
 // Decode-step benchmark on MI355X: the paged fused kernels vs the naive 3-pass kernels, CSV on
 // stdout (the reference's bench/bench.cpp, GPU side). GPU time is a hipEvent pair around each
-// step; caches are flushed (1 GiB overwrite) before every timed run unless --no-flush; runs are
+// step; caches are flushed (1 GiB streaming read) before every timed run unless --no-flush; runs are
 // queued back to back (pipelined) unless --sync; the median of --reps runs is reported.
 // --chain=N times N back-to-back steps per submission with warm caches (run_paged_steps).
 // --bw runs the read-bandwidth probe. --config=c1..c5 selects a BASELINE configuration (N(0,1)
@@ -90,8 +90,8 @@ int main(int argc, char** argv) {
     // The BASELINE configurations (fixed lengths; c5's ragged batch is bench.py's).
     if (config == "c1") shape = {1, 32, 8, 128}, lens = {512}, pages = {16}, parts = {128}, types = {KvType::f32}, pool = 2.0, dist = Dist::normal;
     else if (config == "c2") shape = {8, 32, 8, 128}, lens = {4096}, pages = {16}, parts = {512}, types = {KvType::f16}, pool = 1.5, dist = Dist::normal;
-    else if (config == "c3") shape = {16, 32, 8, 128}, lens = {8192}, pages = {64}, parts = {0}, types = {KvType::i8}, pool = 1.0, dist = Dist::normal;
-    else if (config == "c4") shape = {4, 64, 8, 128}, lens = {32768}, pages = {128}, parts = {2048}, types = {KvType::f16}, pool = 1.25, dist = Dist::normal;
+    else if (config == "c3") shape = {16, 32, 8, 128}, lens = {8192}, pages = {64}, parts = {mi355x_part_tokens({16, 32, 8, 128}, 8192, mi355x_min_groups(KvType::i8))}, types = {KvType::i8}, pool = 1.0, dist = Dist::normal;
+    else if (config == "c4") shape = {4, 64, 8, 128}, lens = {32768}, pages = {128}, parts = {mi355x_part_tokens({4, 64, 8, 128}, 32768)}, types = {KvType::f16}, pool = 1.25, dist = Dist::normal;
     else if (!config.empty()) {
         std::fprintf(stderr, "unknown config %s (c1..c4)\n", config.c_str());
         return 2;

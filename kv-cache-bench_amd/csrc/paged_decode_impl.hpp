@@ -48,6 +48,10 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// Pointers into the constant address space (4): loads through them may be scalar (s_load).
+typedef __attribute__((address_space(4))) const int32_t* const_i32;
+typedef __attribute__((address_space(4))) const float* const_f32;
+
 // Buffer-instruction cache policy sc1: device (agent) scope, coherent across the XCDs' L2s.
 constexpr int kScopeAgent = 16;
 constexpr float kNegBig = -1e30f;  // "minus infinity" that keeps exp2(kNegBig - m) == 0 and no inf - inf
@@ -168,8 +172,10 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
     constexpr int NJ = T::NJ, VL = T::VL, NV = T::NV, NMB = D / 16;
     constexpr bool F32 = KIND == KV_F32;
     static_assert(QG == 1 || QG == 2 || QG == 4 || QG == 8, "QG must be 1, 2, 4 or 8");
-    // double-buffer the tile registers unless that would not fit (fp32 caches)
-    constexpr bool DOUBLE = !F32;
+    // Tile register buffers per wave: one computed, NBUF - 1 in flight. fp32 tiles are too large
+    // for more than one; int8 tiles are half an fp16 tile, so int8 keeps three to have as many
+    // bytes in flight as fp16 does with two.
+    constexpr int NBUF = F32 ? 1 : (KIND == KV_I8 ? 3 : 2);
 
     // Per wave: the V tile (32 rows of D elements, swizzled); after the loop it holds the wave's
     // final accumulators [QG][D] fp32 for the merge (QG * D * 4 <= 32 * D * LDS_ESZ bytes).
@@ -194,59 +200,15 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, q4 = lane >> 4;  // MFMA: column (stack row of q) / token row, row quad
-    const int32_t* bt = p.block_table + (size_t)b * p.max_blocks;
+    // The block table and the int8 scales are read through the constant address space: nothing
+    // writes them during the kernel, and that lets the wave-uniform reads be scalar loads, whose
+    // counter (lgkmcnt) is separate from the K/V loads'. As vector loads, the wait for a block id
+    // (vmcnt counts in order) would also wait for every tile still in flight.
+    const const_i32 bt = (const_i32)p.block_table + (size_t)b * p.max_blocks;
+    const const_f32 ksc = (const_f32)p.k_scale, vsc = (const_f32)p.v_scale;
     const char* kbase = static_cast<const char*>(p.k);
     const char* vbase = static_cast<const char*>(p.v);
     unsigned char* vt = s_v[wave];
-
-    // ---- q as the B operand of S^T = K Q^T: column c holds head c/2, high (c even) or low part.
-    const int hh = c >> 1, hl = c & 1;
-    const bool qcol = hh < QG;
-    const float* qp = p.q + ((size_t)b * H + h0 + (qcol ? hh : 0)) * D;
-    float up = 1.0f;  // scores are MFMA results times `up` (a power of two)
-    half8_t aq16[F32 ? 1 : NJ];
-    float aq32[F32 ? NJ : 1];
-    if constexpr (F32) {
-        for (int j = 0; j < NJ; ++j) aq32[j] = (qcol && hl == 0) ? qp[T::dslot(j, q4, 0)] * p.qscale : 0.0f;
-    } else {
-        float qv[NJ][8];
-        float amax = 0.0f;
-        for (int j = 0; j < NJ; ++j)
-            for (int s = 0; s < 8; ++s) {
-                qv[j][s] = qcol ? qp[T::dslot(j, q4, s)] * p.qscale : 0.0f;
-                amax = fmaxf(amax, fabsf(qv[j][s]));
-            }
-        amax = wave_max(amax);
-        int e = 0;
-        if (amax > 0.0f) {
-            frexpf(amax, &e);  // amax < 2^e
-            e -= 14;           // the scaled q stays below 2^14, far from fp16 overflow
-        }
-        const float down = ldexpf(1.0f, -e);
-        up = ldexpf(1.0f, e);
-        for (int j = 0; j < NJ; ++j)
-            for (int s = 0; s < 8; ++s) {
-                const float x = qv[j][s] * down;
-                const _Float16 hi = (_Float16)x;
-                const _Float16 lo = (_Float16)(x - (float)hi);
-                aq16[j][s] = hl ? lo : hi;
-            }
-    }
-
-    // ---- int8: p * v_scale is split into fp16 high and low parts for the P*V MFMA. Normalise it by
-    // a power of two 2^-ve (ve: the exponent of the largest V scale of the partition) so it stays in
-    // fp16's normal range however small the scales are; the accumulators are rescaled by 2^ve at the
-    // end (exact).
-    float vdown = 1.0f, vupf = 1.0f;
-    if constexpr (KIND == KV_I8) {
-        float vmx = 0.0f;
-        for (int i = t0 / P + lane; i <= (t1 - 1) / P; i += 64) vmx = fmaxf(vmx, p.v_scale[(size_t)bt[i] * Hkv + kvh]);
-        vmx = wave_max(vmx);
-        int ve = 0;
-        if (vmx > 0.0f) frexpf(vmx, &ve);  // vmx < 2^ve
-        vdown = ldexpf(1.0f, -ve);
-        vupf = ldexpf(1.0f, ve);
-    }
 
     // ---- tile loads (no branches around them, so the compiler can keep a tile in flight)
     auto load_tile = [&](R& r, int tt) {
@@ -273,8 +235,8 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
                     r.v[h][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
                                                               rv, (i * (64 / VL) + lane / VL) * D * T::ESZ + (lane % VL) * 16, 0, kNonTemporal));
                 if constexpr (KIND == KV_I8) {
-                    r.ks[h] = p.k_scale[(size_t)blk * Hkv + kvh];
-                    r.vs[h] = p.v_scale[(size_t)blk * Hkv + kvh];
+                    r.ks[h] = ksc[(size_t)blk * Hkv + kvh];
+                    r.vs[h] = vsc[(size_t)blk * Hkv + kvh];
                 }
             } else {
                 // Any page size: each lane finds the block of its own token. Lanes past t1 read the
@@ -301,13 +263,69 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
                         const int ts = th + 4 * q4 + i;
                         const int tss = ts < t1 ? ts : t0;
                         const size_t slot = (size_t)bt[tss / P] * Hkv + kvh;
-                        r.ks[4 * h + i] = p.k_scale[slot];
-                        r.vs[4 * h + i] = p.v_scale[slot];
+                        r.ks[4 * h + i] = ksc[slot];
+                        r.vs[4 * h + i] = vsc[slot];
                     }
                 }
             }
         }
     };
+
+    // ---- q as the B operand of S^T = K Q^T: column c holds head c/2, high (c even) or low part.
+    // Its loads go out first, then the wave's first NBUF - 1 tiles; the q split then runs under
+    // the tiles' latency. (vmcnt counts loads in the order they were issued: a q load issued
+    // after the tiles could only be waited for together with them.)
+    const int hh = c >> 1, hl = c & 1;
+    const bool qcol = hh < QG;
+    const float* qp = p.q + ((size_t)b * H + h0 + (qcol ? hh : 0)) * D;
+    float up = 1.0f;  // scores are MFMA results times `up` (a power of two)
+    half8_t aq16[F32 ? 1 : NJ];
+    float aq32[F32 ? NJ : 1];
+    constexpr int QS = F32 ? 1 : 8;  // q elements per MFMA slot
+    float qv[NJ][QS];                // raw loads only: any use before the barrier below would wait for them
+    for (int j = 0; j < NJ; ++j)
+        for (int s = 0; s < QS; ++s) qv[j][s] = qp[T::dslot(j, q4, s)];
+
+    const int ntiles = (t1 - t0 + kTok - 1) / kTok;
+    int it = wave;
+    R r[NBUF];
+    for (int k = 0; k + 1 < NBUF; ++k) load_tile(r[k], t0 + (it + k * W) * kTok);
+    // (an empty asm with a memory clobber: without it the tile loads are sunk past the q split, to
+    // their first use, and the q loads past the tiles')
+    asm volatile("" ::: "memory");
+
+    for (int j = 0; j < NJ; ++j)
+        for (int s = 0; s < QS; ++s) qv[j][s] = (qcol && (!F32 || hl == 0)) ? qv[j][s] * p.qscale : 0.0f;
+    if constexpr (F32) {
+        for (int j = 0; j < NJ; ++j) aq32[j] = qv[j][0];
+    } else {
+        float amax = 0.0f;
+        for (int j = 0; j < NJ; ++j)
+            for (int s = 0; s < 8; ++s) amax = fmaxf(amax, fabsf(qv[j][s]));
+        amax = wave_max(amax);
+        int e = 0;
+        if (amax > 0.0f) {
+            frexpf(amax, &e);  // amax < 2^e
+            e -= 14;           // the scaled q stays below 2^14, far from fp16 overflow
+        }
+        const float down = ldexpf(1.0f, -e);
+        up = ldexpf(1.0f, e);
+        for (int j = 0; j < NJ; ++j)
+            for (int s = 0; s < 8; ++s) {
+                const float x = qv[j][s] * down;
+                const _Float16 hi = (_Float16)x;
+                const _Float16 lo = (_Float16)(x - (float)hi);
+                aq16[j][s] = hl ? lo : hi;
+            }
+    }
+
+    // ---- int8: p * v_scale is split into fp16 high and low parts for the P*V MFMA. It is
+    // normalised by 2^-ve, ve the exponent of the largest V scale the wave has met so far, so it
+    // stays in fp16's normal range however small the scales are; when a tile brings a larger
+    // scale the accumulators are rescaled by the (exact) power of two, as for a new running max,
+    // and at the end they are scaled by 2^ve. (ve starts below every float exponent: 2^-160 is 0.)
+    float vdown = 1.0f;
+    int ve = -160;
 
     // ---- V tile -> LDS (row-major, swizzled 16-byte chunks; int8 widened to fp16)
     auto store_v = [&](const R& r) {
@@ -354,6 +372,21 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
                     const half8_t kb = (j & 1) ? i8x8_to_half8(w4.z, w4.w) : i8x8_to_half8(w4.x, w4.y);
                     S[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb, aq16[j], S[h], 0, 0, 0);
                 }
+            }
+        }
+        if constexpr (KIND == KV_I8) {
+            float vmx = FAST ? fmaxf(r.vs[0], r.vs[1]) : 0.0f;
+            if constexpr (!FAST) {
+                for (int j = 0; j < 8; ++j) vmx = fmaxf(vmx, r.vs[j]);
+                vmx = wave_max(vmx);
+            }
+            int e = ve;
+            if (vmx > 0.0f) frexpf(vmx, &e);  // vmx < 2^e
+            if (e > ve) {  // wave-uniform
+                const float down = ldexpf(1.0f, ve - e);
+                for (int mb = 0; mb < NMB; ++mb) acc[mb] *= down;
+                ve = e;
+                vdown = ldexpf(1.0f, -e);
             }
         }
         // scores of this lane's 8 tokens for head c/2: high + low columns, scaled, masked
@@ -423,35 +456,24 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    // ---- walk the tiles. The prefetch is unconditional (past the end it reads zeros) so no
-    // branch splits the load counters the compiler tracks.
-    const int ntiles = (t1 - t0 + kTok - 1) / kTok;
-    int it = wave;
-    if constexpr (DOUBLE) {
-        R ra, rb;
-        load_tile(ra, t0 + it * kTok);
-        // (sched_barrier: the scheduler would otherwise sink part of the prefetch below the wait
-        // for the tile being computed, leaving less in flight)
-        while (it < ntiles) {
-            load_tile(rb, t0 + (it + W) * kTok);
-            __builtin_amdgcn_sched_barrier(0);
-            compute_tile(ra, t0 + it * kTok);
-            it += W;
+    // ---- walk the tiles, NBUF - 1 tiles in flight while one is computed: buffer k holds the
+    // tiles it, it + NBUF*W, ... The prefetch is unconditional (past the end it reads zeros) so no
+    // branch splits the load counters the compiler tracks. (sched_barrier: the scheduler would
+    // otherwise sink part of the prefetch below the wait for the tile being computed, leaving
+    // less in flight)
+    while (it < ntiles) {
+#pragma unroll
+        for (int k = 0; k < NBUF; ++k) {
             if (it >= ntiles) break;
-            load_tile(ra, t0 + (it + W) * kTok);
+            load_tile(r[(k + NBUF - 1) % NBUF], t0 + (it + (NBUF - 1) * W) * kTok);
             __builtin_amdgcn_sched_barrier(0);
-            compute_tile(rb, t0 + it * kTok);
+            compute_tile(r[k], t0 + it * kTok);
             it += W;
-        }
-    } else {
-        R ra;
-        for (; it < ntiles; it += W) {
-            load_tile(ra, t0 + it * kTok);
-            compute_tile(ra, t0 + it * kTok);
         }
     }
 
     // ---- merge: lanes -> wave state -> workgroup
+    const float vupf = KIND == KV_I8 ? ldexpf(1.0f, ve) : 1.0f;
     l = sum_x16_x32(l);
     float* sacc = reinterpret_cast<float*>(vt);  // reuse the wave's V tile: [QG][D]
     for (int mb = 0; mb < NMB; ++mb)
@@ -502,50 +524,59 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
     __syncthreads();
     if (!s_last) return;
 
-    // (m_i, l_i) of the group's partitions into LDS (the V tiles are free again), all loads in flight
-    // at once; then w_i in place of l_i; then each thread sums 16-byte rows of part_out, eight
-    // partitions' loads in flight per batch. The merge is on the step's critical path: it starts
-    // when the last partition ends, so its latency, not its few bytes, is what costs.
+    // The merge is on the step's critical path (it starts when the last partition ends), so its
+    // latency, not its few bytes, is what costs: one round trip for everything where possible.
+    // Thread e owns the 16-byte column chunk e of the group's [QG][D] output. It issues its rows
+    // of the first kPre partitions at once, together with the (m_i, l_i) of all partitions into
+    // LDS (the V tiles are free again); then w_i replaces l_i; then the sums, in partition order,
+    // with any partitions past kPre in batches of kBatch.
     static_assert(sizeof(s_v) / sizeof(float2) == fused_merge_slots(KIND, D), "merge staging size");
+    static_assert(QG * D / 4 <= 64 * W, "one 16-byte output chunk per thread");
+    constexpr int kPre = 16, kBatch = 8;
     float2* s_pml = reinterpret_cast<float2*>(&s_v[0][0]);  // [QG][nparts]
     const size_t gbase = ((size_t)b * H + h0) * p.max_parts;  // first slot of head h0
-    for (int e = threadIdx.x; e < QG * nparts; e += 64 * W) {
-        const size_t slot = gbase + (size_t)(e / nparts) * p.max_parts + e % nparts;
-        s_pml[e] = make_float2(load_agent(&p.part_ml[slot].x), load_agent(&p.part_ml[slot].y));
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < QG * nparts; e += 64 * W) {
-        const float2* row = s_pml + (e / nparts) * nparts;
-        float M = kNegBig;
-        for (int i = 0; i < nparts; ++i) M = fmaxf(M, row[i].x);
-        s_pml[e].y = partition_weight(s_pml[e].x, s_pml[e].y, M);
-    }
-    __syncthreads();
-    constexpr int kBatch = 8;
     const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(
         p.part_out + gbase * D, (short)0, QG * p.max_parts * D * 4, 0x00020000);
-    for (int e = threadIdx.x; e < QG * D / 4; e += 64 * W) {
-        const int h = e / (D / 4), d4 = e % (D / 4);
-        const float2* wrow = s_pml + h * nparts;
+    const int e = threadIdx.x, eh = e / (D / 4), ed = e % (D / 4);
+    const bool owner = e < QG * D / 4;
+    auto row = [&](int i) {  // partition i's chunk of this thread (zeros past the group's slots)
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rpo, ((eh * p.max_parts + i) * D + 4 * ed) * 4, 0, kScopeAgent));
+    };
+    float4 pre[kPre];
+    for (int j = 0; j < kPre; ++j) pre[j] = row(j);  // slots past nparts are read and ignored
+    for (int x = threadIdx.x; x < QG * nparts; x += 64 * W) {
+        const size_t slot = gbase + (size_t)(x / nparts) * p.max_parts + x % nparts;
+        s_pml[x] = make_float2(load_agent(&p.part_ml[slot].x), load_agent(&p.part_ml[slot].y));
+    }
+    __syncthreads();
+    for (int x = threadIdx.x; x < QG * nparts; x += 64 * W) {
+        const float2* mrow = s_pml + (x / nparts) * nparts;
+        float M = kNegBig;
+        for (int i = 0; i < nparts; ++i) M = fmaxf(M, mrow[i].x);
+        s_pml[x].y = partition_weight(s_pml[x].x, s_pml[x].y, M);
+    }
+    __syncthreads();
+    if (owner) {
+        const float2* wrow = s_pml + eh * nparts;
         float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         float L = 0.0f;
-        for (int i0 = 0; i0 < nparts; i0 += kBatch) {
+        auto add = [&](float wt, const float4& v) {
+            L += wt;
+            o.x = __builtin_fmaf(wt, v.x, o.x);
+            o.y = __builtin_fmaf(wt, v.y, o.y);
+            o.z = __builtin_fmaf(wt, v.z, o.z);
+            o.w = __builtin_fmaf(wt, v.w, o.w);
+        };
+        for (int j = 0; j < kPre; ++j)
+            if (j < nparts) add(wrow[j].y, pre[j]);
+        for (int i0 = kPre; i0 < nparts; i0 += kBatch) {
             float4 v[kBatch];
+            for (int j = 0; j < kBatch; ++j) v[j] = row(i0 + j);
             for (int j = 0; j < kBatch; ++j)
-                if (i0 + j < nparts)
-                    v[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                          rpo, ((h * p.max_parts + i0 + j) * D + 4 * d4) * 4, 0, kScopeAgent));
-            for (int j = 0; j < kBatch; ++j)
-                if (i0 + j < nparts) {
-                    const float wt = wrow[i0 + j].y;
-                    L += wt;
-                    o.x = __builtin_fmaf(wt, v[j].x, o.x);
-                    o.y = __builtin_fmaf(wt, v[j].y, o.y);
-                    o.z = __builtin_fmaf(wt, v[j].z, o.z);
-                    o.w = __builtin_fmaf(wt, v[j].w, o.w);
-                }
+                if (i0 + j < nparts) add(wrow[i0 + j].y, v[j]);
         }
-        *reinterpret_cast<float4*>(p.out + ((size_t)b * H + h0 + h) * D + 4 * d4) =
+        *reinterpret_cast<float4*>(p.out + ((size_t)b * H + h0 + eh) * D + 4 * ed) =
             make_float4(o.x / L, o.y / L, o.z / L, o.w / L);
     }
     if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -42,7 +42,7 @@ def test_baseline_config_full_size(gpu, oracle, name):
     kvb = gpu
     w, c, cfg = kvb.make_config(name, poison=True, threads=THREADS)
     progress(f"[parity] {name}: B={w.shape.batch} max_len={w.max_len} tokens={int(w.lens.sum())} pool={c.num_blocks}")
-    part = cfg["part"]
+    part = kvb.config_part(cfg, w)
     got = run(kvb, w, c, part)
     want, tol = expected(kvb, oracle, w, c)
     err = oracle.max_abs_diff(got, want)

@@ -70,11 +70,19 @@ def test_poison_marks_every_unowned_element(kvb):
 
 
 def test_mi355x_partition_policy(kvb):
-    # c4 (B 4, 64/8 heads, 32k): 4 * 8 groups per partition -> 1024 groups at part 1024.
-    assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768) == 1024
-    assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768, min_groups=512) == 2048
+    # c4 (B 4, 64/8 heads, 32k): 4 * 8 workgroups per partition -> 256 at part 4096 (fp16 target),
+    # 512 at part 2048 (int8 target).
+    assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768) == 4096
+    assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768, min_groups=kvb.mi355x_min_groups(kvb.KV_I8)) == 2048
+    assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768, min_groups=1024) == 1024
+    # short or small: the floor
     assert kvb.mi355x_part_tokens(kvb.Shape(1, 32, 8, 128), 512) == 256
-    assert kvb.mi355x_part_tokens(kvb.Shape(16, 32, 8, 128), 8192) == 1024
+    # c3 (B 16, 32/8 heads, 8k): 16 * 8 workgroups per partition
+    assert kvb.mi355x_part_tokens(kvb.Shape(16, 32, 8, 128), 8192) == 4096
+    assert kvb.mi355x_part_tokens(kvb.Shape(16, 32, 8, 128), 8192, min_groups=512) == 2048
+    # BASELINE names c1's and c2's partitions; the policy is used where it leaves the choice
+    assert kvb.CONFIGS["c1"]["part"] == 128 and kvb.CONFIGS["c2"]["part"] == 512
+    assert all(kvb.CONFIGS[n]["part"] == "mi355x" for n in ("c3", "c4", "c5f16", "c5i8"))
 
 
 class TestRefusals:
