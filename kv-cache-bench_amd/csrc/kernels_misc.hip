@@ -122,27 +122,29 @@ __global__ __launch_bounds__(256) void fill_kernel(uint4* dst, size_t n16, uint3
 
 }  // namespace
 
-hipError_t launch_paged_reduce(int head_dim, const ReduceParams& p, int batch, hipStream_t s) {
+hipError_t launch_paged_reduce(int head_dim, const ReduceParams& p, int batch, hipStream_t s, const Marks& m) {
     const dim3 grid(p.num_heads, batch);
-    if (head_dim == 64) hipLaunchKernelGGL(paged_reduce_kernel<64>, grid, dim3(64), 0, s, p);
-    else if (head_dim == 128) hipLaunchKernelGGL(paged_reduce_kernel<128>, grid, dim3(128), 0, s, p);
+    if (head_dim == 64) launch_marked(paged_reduce_kernel<64>, grid, dim3(64), s, m, p);
+    else if (head_dim == 128) launch_marked(paged_reduce_kernel<128>, grid, dim3(128), s, m, p);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
-hipError_t launch_naive(int kind, int head_dim, int group, const NaiveParams& p, int batch, hipStream_t s) {
+hipError_t launch_naive(int kind, int head_dim, int group, const NaiveParams& p, int batch, hipStream_t s,
+                        const Marks& m) {
     const dim3 sgrid((unsigned)((p.max_len > 0 ? p.max_len : 1) + 255) / 256, p.num_heads, batch);
-    if (kind == KV_F16) hipLaunchKernelGGL(naive_scores_kernel<KV_F16>, sgrid, dim3(256), 0, s, p, head_dim, group);
-    else hipLaunchKernelGGL(naive_scores_kernel<KV_F32>, sgrid, dim3(256), 0, s, p, head_dim, group);
+    const Marks first{m.start, nullptr}, last{nullptr, m.stop};
+    if (kind == KV_F16) launch_marked(naive_scores_kernel<KV_F16>, sgrid, dim3(256), s, first, p, head_dim, group);
+    else launch_marked(naive_scores_kernel<KV_F32>, sgrid, dim3(256), s, first, p, head_dim, group);
     hipLaunchKernelGGL(naive_softmax_kernel, dim3(p.num_heads, batch), dim3(256), 0, s, p);
-    if (kind == KV_F16) hipLaunchKernelGGL(naive_pv_kernel<KV_F16>, dim3(p.num_heads, batch), dim3(head_dim), 0, s, p, head_dim, group);
-    else hipLaunchKernelGGL(naive_pv_kernel<KV_F32>, dim3(p.num_heads, batch), dim3(head_dim), 0, s, p, head_dim, group);
+    if (kind == KV_F16) launch_marked(naive_pv_kernel<KV_F16>, dim3(p.num_heads, batch), dim3(head_dim), s, last, p, head_dim, group);
+    else launch_marked(naive_pv_kernel<KV_F32>, dim3(p.num_heads, batch), dim3(head_dim), s, last, p, head_dim, group);
     return hipGetLastError();
 }
 
-hipError_t launch_read_bw(const void* src, size_t n16, float* sink, hipStream_t s) {
+hipError_t launch_read_bw(const void* src, size_t n16, float* sink, hipStream_t s, const Marks& m) {
     // 32768 workgroups: the fastest shape of a sweep over 512..32768 on MI355X (~7.0 TB/s)
-    hipLaunchKernelGGL(read_bw_kernel, dim3(kReadBwGroups), dim3(256), 0, s, static_cast<const u32x4_t*>(src), n16, sink);
+    launch_marked(read_bw_kernel, dim3(kReadBwGroups), dim3(256), s, m, static_cast<const u32x4_t*>(src), n16, sink);
     return hipGetLastError();
 }
 

@@ -1,6 +1,7 @@
 // Launch parameters and launcher declarations shared by the gfx950 kernels and the runtime.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -80,24 +81,45 @@ struct NaiveParams {
     float scale;
 };
 
+// Timing marks of a launch: events that the kernel dispatch itself stamps with its start and end
+// (hipExtLaunchKernelGGL), so a pair brackets the kernels' execution and not the launch gap before
+// the first one (the reference's GPUStartTime / GPUEndTime, src/metal_attn.mm:119-130).
+struct Marks {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+
+template <typename... KArgs, typename... Args>
+inline void launch_marked(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t s, const Marks& m,
+                          Args... args) {
+    if (m.start || m.stop)
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, s, m.start, m.stop, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
+}
+
 // paged_decode for one storage kind: grid (max_parts, H / qg, batch), kDecodeWaves waves per
 // workgroup. `fast`: every 16-token tile lies inside one page (page_size % 16 == 0 and
 // part_tokens % 16 == 0), so block ids and scales are read once per tile.
-hipError_t launch_paged_decode_f32(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s);
-hipError_t launch_paged_decode_f16(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s);
-hipError_t launch_paged_decode_i8(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s);
+hipError_t launch_paged_decode_f32(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s,
+                                   const Marks& m = {});
+hipError_t launch_paged_decode_f16(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s,
+                                   const Marks& m = {});
+hipError_t launch_paged_decode_i8(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s,
+                                  const Marks& m = {});
 
 // paged_reduce: grid (H, batch), head_dim threads.
-hipError_t launch_paged_reduce(int head_dim, const ReduceParams& p, int batch, hipStream_t s);
+hipError_t launch_paged_reduce(int head_dim, const ReduceParams& p, int batch, hipStream_t s, const Marks& m = {});
 
 // The naive three-pass baseline over a contiguous cache (f32 or f16).
-hipError_t launch_naive(int kind, int head_dim, int group, const NaiveParams& p, int batch, hipStream_t s);
+hipError_t launch_naive(int kind, int head_dim, int group, const NaiveParams& p, int batch, hipStream_t s,
+                        const Marks& m = {});
 
 // Streaming read of n16 16-byte words over kReadBwGroups workgroups; the guarded store into sink
 // (kReadBwSink floats) never fires for real data.
 constexpr int kReadBwGroups = 32768;
 constexpr size_t kReadBwSink = 2048 * 256;
-hipError_t launch_read_bw(const void* src, size_t n16, float* sink, hipStream_t s);
+hipError_t launch_read_bw(const void* src, size_t n16, float* sink, hipStream_t s, const Marks& m = {});
 // Overwrites n16 16-byte words with `value`.
 hipError_t launch_fill(void* dst, size_t n16, uint32_t value, hipStream_t s);
 

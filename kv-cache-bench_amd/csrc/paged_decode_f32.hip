@@ -4,8 +4,9 @@
 
 namespace kvbk {
 
-hipError_t launch_paged_decode_f32(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s) {
-    return launch_for_kind<KV_F32>(head_dim, qg, fast, p, batch, s);
+hipError_t launch_paged_decode_f32(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s,
+                                  const Marks& m) {
+    return launch_for_kind<KV_F32>(head_dim, qg, fast, p, batch, s, m);
 }
 
 }  // namespace kvbk

@@ -583,27 +583,28 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
 }
 
 template <int KIND, int D, int QG, bool FAST>
-hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s) {
+hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
     const dim3 grid(p.max_parts, p.num_heads / QG, batch);
-    hipLaunchKernelGGL((paged_decode_kernel<KIND, D, QG, FAST>), grid, dim3(64 * kDecodeWaves), 0, s, p);
+    launch_marked(paged_decode_kernel<KIND, D, QG, FAST>, grid, dim3(64 * kDecodeWaves), s, m, p);
     return hipGetLastError();
 }
 
 template <int KIND, int D>
-hipError_t launch_for_dim(int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s) {
+hipError_t launch_for_dim(int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
     switch (qg) {
-        case 1: return fast ? launch_one<KIND, D, 1, true>(p, batch, s) : launch_one<KIND, D, 1, false>(p, batch, s);
-        case 2: return fast ? launch_one<KIND, D, 2, true>(p, batch, s) : launch_one<KIND, D, 2, false>(p, batch, s);
-        case 4: return fast ? launch_one<KIND, D, 4, true>(p, batch, s) : launch_one<KIND, D, 4, false>(p, batch, s);
-        case 8: return fast ? launch_one<KIND, D, 8, true>(p, batch, s) : launch_one<KIND, D, 8, false>(p, batch, s);
+        case 1: return fast ? launch_one<KIND, D, 1, true>(p, batch, s, m) : launch_one<KIND, D, 1, false>(p, batch, s, m);
+        case 2: return fast ? launch_one<KIND, D, 2, true>(p, batch, s, m) : launch_one<KIND, D, 2, false>(p, batch, s, m);
+        case 4: return fast ? launch_one<KIND, D, 4, true>(p, batch, s, m) : launch_one<KIND, D, 4, false>(p, batch, s, m);
+        case 8: return fast ? launch_one<KIND, D, 8, true>(p, batch, s, m) : launch_one<KIND, D, 8, false>(p, batch, s, m);
         default: return hipErrorInvalidValue;
     }
 }
 
 template <int KIND>
-hipError_t launch_for_kind(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s) {
-    if (head_dim == 64) return launch_for_dim<KIND, 64>(qg, fast, p, batch, s);
-    if (head_dim == 128) return launch_for_dim<KIND, 128>(qg, fast, p, batch, s);
+hipError_t launch_for_kind(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s,
+                           const Marks& m) {
+    if (head_dim == 64) return launch_for_dim<KIND, 64>(qg, fast, p, batch, s, m);
+    if (head_dim == 128) return launch_for_dim<KIND, 128>(qg, fast, p, batch, s, m);
     return hipErrorInvalidValue;
 }
 

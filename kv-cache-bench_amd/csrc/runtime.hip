@@ -159,18 +159,25 @@ int query_heads_per_group(const kvb_paged_args* a) {
 
 // Grows the fused-merge counters to B * H ints, zeroed (the kernel leaves them at 0).
 int counters_for(const kvb_paged_args* a, int** out) {
-    const size_t need = (size_t)a->batch * a->num_heads * sizeof(int);
+    const size_t need = ((size_t)a->batch * a->num_heads * sizeof(int) + 15) / 16 * 16;  // whole fill words
     if (g.counters_bytes < need || !g.counters) {
         if (int st = grow(&g.counters, &g.counters_bytes, need)) return st;
-        KVB_HIP(hipMemsetAsync(g.counters, 0, g.counters_bytes, g.stream));
+        // zeroed once here (a fill kernel, not a memset node); each fused launch leaves them at 0
+        if (hipError_t e = kvbk::launch_fill(g.counters, g.counters_bytes / 16, 0u, g.stream); e != hipSuccess)
+            return fail(KVB_ERUNTIME, std::string("counter fill: ") + hipGetErrorString(e));
     }
     *out = static_cast<int*>(g.counters);
     return KVB_OK;
 }
 
 // Queues one decode step. fused: one paged_decode that also merges the partitions; otherwise
-// paged_decode then paged_reduce, with e_mid (if given) recorded between them.
-int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, bool fused, hipEvent_t e_mid) {
+// paged_decode then paged_reduce. `step` marks the start of the step's first kernel and the end of
+// its last; `decode` and `reduce` (two-kernel form only) mark each kernel.
+struct StepMarks {
+    kvbk::Marks step, decode, reduce;
+};
+
+int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, bool fused, const StepMarks& mk) {
     const int part = resolve_part(a);
     const int qg = query_heads_per_group(a);
     kvbk::DecodeParams p{};
@@ -198,17 +205,18 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
         if (int st = counters_for(a, &p.counters)) return st;
     }
     const bool fast = a->page_size % kvbk::kTile == 0 && part % kvbk::kTile == 0;
+    const kvbk::Marks dm{mk.step.start ? mk.step.start : mk.decode.start, fused ? mk.step.stop : mk.decode.stop};
+    const kvbk::Marks rm{mk.reduce.start, mk.step.stop ? mk.step.stop : mk.reduce.stop};
     hipError_t e = hipSuccess;
     switch (a->kv_type) {
-        case KVB_KV_F32: e = kvbk::launch_paged_decode_f32(a->head_dim, qg, fast, p, a->batch, g.stream); break;
-        case KVB_KV_F16: e = kvbk::launch_paged_decode_f16(a->head_dim, qg, fast, p, a->batch, g.stream); break;
-        default: e = kvbk::launch_paged_decode_i8(a->head_dim, qg, fast, p, a->batch, g.stream); break;
+        case KVB_KV_F32: e = kvbk::launch_paged_decode_f32(a->head_dim, qg, fast, p, a->batch, g.stream, dm); break;
+        case KVB_KV_F16: e = kvbk::launch_paged_decode_f16(a->head_dim, qg, fast, p, a->batch, g.stream, dm); break;
+        default: e = kvbk::launch_paged_decode_i8(a->head_dim, qg, fast, p, a->batch, g.stream, dm); break;
     }
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("paged_decode launch: ") + hipGetErrorString(e));
     if (fused) return KVB_OK;
-    if (e_mid) KVB_HIP(hipEventRecord(e_mid, g.stream));
     kvbk::ReduceParams r{part_out, part_ml, a->seq_lens, a->out, a->num_heads, p.max_parts, part};
-    e = kvbk::launch_paged_reduce(a->head_dim, r, a->batch, g.stream);
+    e = kvbk::launch_paged_reduce(a->head_dim, r, a->batch, g.stream, rm);
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("paged_reduce launch: ") + hipGetErrorString(e));
     return KVB_OK;
 }
@@ -335,10 +343,11 @@ int kvb_run_paged_steps(const kvb_paged_args* a, int steps, double* ms) {
     hipEvent_t e0, e1;
     if (int st = get_event(&e0)) return st;
     if (int st = get_event(&e1)) return st;
-    KVB_HIP(hipEventRecord(e0, g.stream));
-    for (int i = 0; i < steps; ++i)
-        if (int st = enqueue_paged(a, part_out, part_ml, true, nullptr)) return st;
-    KVB_HIP(hipEventRecord(e1, g.stream));
+    for (int i = 0; i < steps; ++i) {
+        StepMarks mk;
+        mk.step = {i == 0 ? e0 : nullptr, i == steps - 1 ? e1 : nullptr};
+        if (int st = enqueue_paged(a, part_out, part_ml, true, mk)) return st;
+    }
     return finish(e0, e1, ms);
 }
 
@@ -353,16 +362,17 @@ int kvb_run_paged_split(const kvb_paged_args* a, double* decode_ms, double* redu
     float* part_out = nullptr;
     float2* part_ml = nullptr;
     if (int st = workspace_for(a, &part_out, &part_ml)) return st;
-    hipEvent_t e[3];
+    hipEvent_t e[4];
     for (auto& x : e)
         if (int st = get_event(&x)) return st;
-    KVB_HIP(hipEventRecord(e[0], g.stream));
-    if (int st = enqueue_paged(a, part_out, part_ml, false, e[1])) return st;
-    KVB_HIP(hipEventRecord(e[2], g.stream));
-    KVB_HIP(hipEventSynchronize(e[2]));
+    StepMarks mk;
+    mk.decode = {e[0], e[1]};
+    mk.reduce = {e[2], e[3]};
+    if (int st = enqueue_paged(a, part_out, part_ml, false, mk)) return st;
+    KVB_HIP(hipEventSynchronize(e[3]));
     float d = 0.0f, r = 0.0f;
     KVB_HIP(hipEventElapsedTime(&d, e[0], e[1]));
-    KVB_HIP(hipEventElapsedTime(&r, e[1], e[2]));
+    KVB_HIP(hipEventElapsedTime(&r, e[2], e[3]));
     for (auto& x : e) g.spare.push_back(x);
     if (decode_ms) *decode_ms = d;
     if (reduce_ms) *reduce_ms = r;
@@ -394,10 +404,9 @@ int kvb_run_naive(const kvb_naive_args* a, double* ms) {
     hipEvent_t e0, e1;
     if (int st = get_event(&e0)) return st;
     if (int st = get_event(&e1)) return st;
-    KVB_HIP(hipEventRecord(e0, g.stream));
-    const hipError_t e = kvbk::launch_naive(a->kv_type, a->head_dim, a->num_heads / a->num_kv_heads, p, a->batch, g.stream);
+    const hipError_t e = kvbk::launch_naive(a->kv_type, a->head_dim, a->num_heads / a->num_kv_heads, p, a->batch,
+                                            g.stream, {e0, e1});
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("naive launch: ") + hipGetErrorString(e));
-    KVB_HIP(hipEventRecord(e1, g.stream));
     return finish(e0, e1, ms);
 }
 
@@ -442,10 +451,8 @@ int kvb_run_read_bandwidth(const void* dev, size_t bytes, double* ms) {
     hipEvent_t e0, e1;
     if (int st = get_event(&e0)) return st;
     if (int st = get_event(&e1)) return st;
-    KVB_HIP(hipEventRecord(e0, g.stream));
-    const hipError_t e = kvbk::launch_read_bw(dev, bytes / 16, g.sink, g.stream);
+    const hipError_t e = kvbk::launch_read_bw(dev, bytes / 16, g.sink, g.stream, {e0, e1});
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("read_bw launch: ") + hipGetErrorString(e));
-    KVB_HIP(hipEventRecord(e1, g.stream));
     return finish(e0, e1, ms);
 }
 
