@@ -105,8 +105,8 @@ struct NaiveArgs {
     const Buffer* out;
 };
 
-// Each call queues the kernels on one stream, waits, and returns their GPU time in milliseconds
-// (a hipEvent pair). Throws std::invalid_argument, before any GPU work, for a sequence length below
+// Each call queues the kernels on one stream, waits, and returns their GPU time in milliseconds,
+// from the first kernel's start to the last kernel's end (events stamped by the dispatches). Throws std::invalid_argument, before any GPU work, for a sequence length below
 // 0, above max_len, or (paged) above max_blocks * page_size, and for the other refusals of
 // kvb_run_paged; std::runtime_error for device failures (src/metal_attn.hpp:82-87).
 double run_paged(const PagedArgs&);
@@ -131,7 +131,7 @@ std::vector<double> end_pipelined();
 // Reads `src` once with a streaming kernel over every CU; returns GPU milliseconds.
 double run_read_bandwidth(const Buffer& src);
 
-// Overwrites a 1 GiB scratch buffer, more than the MALL and L2s hold, so the next run starts cold.
+// Reads a 1 GiB scratch buffer, more than the MALL and L2s hold, so the next run starts cold.
 void flush_gpu_caches();
 
 // The C ABI view of `a` (device pointers resolved, host writes uploaded).
