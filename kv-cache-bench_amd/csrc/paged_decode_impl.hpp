@@ -173,9 +173,9 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
     constexpr bool F32 = KIND == KV_F32;
     static_assert(QG == 1 || QG == 2 || QG == 4 || QG == 8, "QG must be 1, 2, 4 or 8");
     // Tile register buffers per wave: one computed, NBUF - 1 in flight. fp32 tiles are too large
-    // for more than one; int8 tiles are half an fp16 tile, so int8 keeps three to have as many
-    // bytes in flight as fp16 does with two.
-    constexpr int NBUF = F32 ? 1 : (KIND == KV_I8 ? 3 : 2);
+    // for more than one. (Three for int8, whose tiles are half an fp16 tile, spill at head_dim 128
+    // and measured slower.)
+    constexpr int NBUF = F32 ? 1 : 2;
 
     // Per wave: the V tile (32 rows of D elements, swizzled); after the loop it holds the wave's
     // final accumulators [QG][D] fp32 for the merge (QG * D * 4 <= 32 * D * LDS_ESZ bytes).
@@ -289,7 +289,13 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
     const int ntiles = (t1 - t0 + kTok - 1) / kTok;
     int it = wave;
     R r[NBUF];
-    for (int k = 0; k + 1 < NBUF; ++k) load_tile(r[k], t0 + (it + k * W) * kTok);
+    for (int k = 0; k + 1 < NBUF; ++k) {
+        load_tile(r[k], t0 + (it + k * W) * kTok);
+        // (in buffer order, as the loop issues them: the loop head is entered from here and from the
+        // back edge, and the wait for buffer 0 there can leave the later buffers in flight only if
+        // both paths issued them in the same order)
+        __builtin_amdgcn_sched_barrier(0);
+    }
     // (an empty asm with a memory clobber: without it the tile loads are sunk past the q split, to
     // their first use, and the q loads past the tiles')
     asm volatile("" ::: "memory");
@@ -457,14 +463,19 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
     };
 
     // ---- walk the tiles, NBUF - 1 tiles in flight while one is computed: buffer k holds the
-    // tiles it, it + NBUF*W, ... The prefetch is unconditional (past the end it reads zeros) so no
-    // branch splits the load counters the compiler tracks. (sched_barrier: the scheduler would
-    // otherwise sink part of the prefetch below the wait for the tile being computed, leaving
-    // less in flight)
-    while (it < ntiles) {
+    // wave's tiles k, k + NBUF, ... The prefetch is unconditional (past the end it reads zeros) so
+    // no branch splits the load counters the compiler tracks. The loop runs whole rounds of NBUF
+    // steps and has one exit: with an exit inside a round, the loop head is also reached from
+    // mid-round paths, where fewer loads are in flight, and its wait for buffer 0 then drains the
+    // later buffers too. The last round may step past the wave's last tile: such a step masks every
+    // score (p = 0, corr = 1 exactly), reads zeros or masked rows, and at most renormalises the
+    // int8 accumulators by a power of two, so it changes nothing. (sched_barrier: the scheduler
+    // would otherwise sink part of the prefetch below the wait for the tile being computed.)
+    const int wtiles = it < ntiles ? (ntiles - it + W - 1) / W : 0;
+    const int rounds = (wtiles + NBUF - 1) / NBUF;
+    for (int rd = 0; rd < rounds; ++rd) {
 #pragma unroll
         for (int k = 0; k < NBUF; ++k) {
-            if (it >= ntiles) break;
             load_tile(r[(k + NBUF - 1) % NBUF], t0 + (it + (NBUF - 1) * W) * kTok);
             __builtin_amdgcn_sched_barrier(0);
             compute_tile(r[k], t0 + it * kTok);
