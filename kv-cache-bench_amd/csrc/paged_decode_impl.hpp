@@ -397,18 +397,21 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
         }
         // scores of this lane's 8 tokens for head c/2: high + low columns, scaled, masked
         float s[8];
-        bool valid[8];
-        float mx = kNegBig;
         for (int h = 0; h < 2; ++h)
             for (int i = 0; i < 4; ++i) {
                 const int j = 4 * h + i;
                 float f = up;
                 if constexpr (KIND == KV_I8) f *= FAST ? r.ks[h] : r.ks[j];
-                const float raw = S[h][i] + dpp<kQuadSwap1>(S[h][i]);
-                valid[j] = tt + h * kHalf + 4 * q4 + i < t1;
-                s[j] = valid[j] ? raw * f : kNegBig;
-                mx = fmaxf(mx, s[j]);
+                s[j] = (S[h][i] + dpp<kQuadSwap1>(S[h][i])) * f;
             }
+        // Tokens past the partition end score kNegBig; only a partition's last tile has any, so the
+        // compare-and-select runs under a wave-uniform branch. (p = exp2(kNegBig - m) below is then
+        // exactly 0: m is finite, since a wave only walks tiles when its first holds a live token.)
+        if (tt + kTok > t1)
+            for (int j = 0; j < 8; ++j)
+                if (tt + kHalf * (j >> 2) + 4 * q4 + (j & 3) >= t1) s[j] = kNegBig;
+        float mx = kNegBig;
+        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, s[j]);
         mx = max_x16_x32(mx);
         const float mn = fmaxf(m, mx);
         const float corr = __builtin_amdgcn_exp2f(m - mn);
@@ -417,7 +420,7 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
         half8_t pb16;
         float pb32[F32 ? 8 : 1];
         for (int j = 0; j < 8; ++j) {
-            const float pr = valid[j] ? __builtin_amdgcn_exp2f(s[j] - mn) : 0.0f;
+            const float pr = __builtin_amdgcn_exp2f(s[j] - mn);
             psum += pr;
             float pv = pr;
             if constexpr (KIND == KV_I8) pv *= (FAST ? r.vs[j >> 2] : r.vs[j]) * vdown;
