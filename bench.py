@@ -171,13 +171,6 @@ def main():
         extras["unfused_reduce_us"] = round(ur * 1e3, 2)
         extras["warm_chain_us"] = round(warm_chain(kvb, dev, part) * 1e3, 2)
         extras["warm_gbps"] = round(bytes_step / (extras["warm_chain_us"] * 1e-6) / 1e9, 1)
-        probe = kvb.Buffer(4 << 30)
-        probe.fill(1)
-        kvb.run_read_bandwidth(probe)
-        pt = [kvb.run_read_bandwidth(probe) for _ in range(5)]
-        extras["probe_gbps"] = round((4 << 30) / (statistics.median(pt) * 1e-3) / 1e9, 1)
-        extras["pct_of_probe"] = round(100 * value / extras["probe_gbps"], 1)
-        probe.free()
     if not args.no_extras and args.config == "c4":
         # the same shape with an int8 cache (per-(page, KV head) scales): the int8 / fp16 speed ratio
         dev.free()
@@ -197,6 +190,15 @@ def main():
         log(f"int8 c4-shape: {medi * 1e3:.1f} us ({extras['int8_speedup_vs_fp16']}x fp16)")
     else:
         dev.free()
+    if not args.no_extras:
+        # the streaming-read ceiling, last: its 4 GiB buffer is freed before nothing else is allocated
+        probe = kvb.Buffer(4 << 30)
+        probe.fill(1)
+        kvb.run_read_bandwidth(probe)
+        pt = [kvb.run_read_bandwidth(probe) for _ in range(5)]
+        extras["probe_gbps"] = round((4 << 30) / (statistics.median(pt) * 1e-3) / 1e9, 1)
+        extras["pct_of_probe"] = round(100 * value / extras["probe_gbps"], 1)
+        probe.free()
 
     cpu = None
     if not args.no_cpu:

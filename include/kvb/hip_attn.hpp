@@ -54,7 +54,9 @@ enum class KvType { f32, f16, i8 };
 inline const char* name(KvType t) { return t == KvType::f32 ? "f32" : t == KvType::f16 ? "f16" : "i8"; }
 inline size_t elem_size(KvType t) { return t == KvType::f32 ? 4 : t == KvType::f16 ? 2 : 1; }
 
-constexpr int kSimdGroups = 4;  // wave64s per paged_decode workgroup (the reference's simdgroups)
+// The reference's simdgroups per workgroup (src/metal_attn.hpp:41). Here paged_decode workgroups
+// have 4 wave64s for f32/f16 caches and 8 for int8.
+constexpr int kSimdGroups = 4;
 
 // Split-K partition size used when PagedArgs::part_tokens is 0 (src/metal_attn.hpp:43-51): the
 // largest power of two in [64, 512] that still yields at least 512 (sequence, KV head,
@@ -68,12 +70,12 @@ inline int auto_part_tokens(const Shape& s, int max_len) {
 // The MI355X partition policy: the largest power of two in [min_part, max_part] whose workgroup
 // count B * ceil(H / qg) * ceil(max_len / part) still reaches `min_groups` (qg: the query heads one
 // workgroup serves). Longer partitions mean fewer partial results to merge and a shorter prologue
-// per token; enough workgroups keep enough bytes in flight. Measured on MI355X (c4): fp16 is
-// fastest at one workgroup per CU (min_groups 256, the default), int8, whose tiles carry half the
-// bytes for the same work, at two (mi355x_min_groups).
+// per token; enough workgroups keep enough bytes in flight. Measured on MI355X (c4): fastest at
+// one workgroup per CU (min_groups 256, the default).
 int mi355x_part_tokens(const Shape& s, int max_len, int min_groups = 256, int min_part = 256, int max_part = 4096);
-// min_groups of the policy for a storage type: 512 for int8, 256 otherwise.
-inline int mi355x_min_groups(KvType t) { return t == KvType::i8 ? 512 : 256; }
+// min_groups of the policy for a storage type: 256 (one workgroup per CU) for every type; an int8
+// workgroup has twice the waves of an fp16 one, so both keep the same waves per SIMD.
+inline int mi355x_min_groups(KvType) { return 256; }
 
 struct PagedArgs {
     Shape shape;

@@ -99,8 +99,8 @@ int kvb_check_paged(const kvb_paged_args* a);
 /* One decode step (run_paged, src/metal_attn.hpp:86): the reference's paged_decode + paged_reduce
  * as one launch of paged_decode whose last workgroup per (sequence, KV-head group) merges the
  * partitions; two kernels (paged_decode, then paged_reduce) when a group's partition count
- * exceeds what that merge stages on chip (query heads per group x max_parts > 1024 for f16/i8 at
- * head_dim 128, 512 at 64; twice that for f32). Either form gives the same bits. *ms = GPU time
+ * exceeds what that merge stages on chip (query heads per group x max_parts > 1024 for f16 at
+ * head_dim 128, 2048 for i8 and f32; half that at head_dim 64). Either form gives the same bits. *ms = GPU time
  * from before the first kernel to after the last (hipEvent pair); 0 in pipelined mode. Refuses (KVB_EINVAL, before any GPU work, output untouched) part_tokens < 0, max_len < 0,
  * page_size <= 0, I8 without scales, a length < 0 or > max_len or > max_blocks * page_size,
  * head_dim not 64/128, H % Hkv != 0 (src/metal_attn.mm:72-73, 107-117, 199-201). */

@@ -155,8 +155,8 @@ def mi355x_part_tokens(shape, max_len, min_groups=256, min_part=256, max_part=40
 
 
 def mi355x_min_groups(kv_type) -> int:
-    """The policy's workgroup target for a storage type: 512 for int8, 256 otherwise."""
-    return 512 if kv_type == KV_I8 else 256
+    """The policy's workgroup target for a storage type (kvb::mi355x_min_groups): 256 for every type."""
+    return 256
 
 
 @dataclass

@@ -11,8 +11,12 @@ namespace kvbk {
 
 enum KvKind { KV_F32 = 0, KV_F16 = 1, KV_I8 = 2 };
 
-// Waves per paged_decode workgroup (the reference's kSimdGroups, src/metal_attn.hpp:41).
-constexpr int kDecodeWaves = 4;
+// Waves per paged_decode workgroup (the reference's kSimdGroups, 4 for every type,
+// src/metal_attn.hpp:41). int8 tiles carry half the bytes of fp16 ones, so an int8 workgroup has 8
+// waves: the same waves per SIMD from half as many partitions, which halves the partial results to
+// merge. Measured on c4-shaped int8: 52 us at 8 waves x 4096-token partitions against 53 us at
+// 4 x 2048; fp16 is best at 4.
+constexpr int decode_waves(int kind) { return kind == KV_I8 ? 8 : 4; }
 // Tokens one wave handles per step of its loop: the N of a 16x16 MFMA tile.
 constexpr int kTile = 16;
 
@@ -55,7 +59,7 @@ __device__ __forceinline__ float partition_weight(float m, float l, float M) {
 // tokens x head_dim per wave, fp32 for f32 caches, fp16 otherwise). Past this the partitions are
 // merged by paged_reduce as a second kernel.
 constexpr int fused_merge_slots(int kind, int head_dim) {
-    return kDecodeWaves * 32 * head_dim * (kind == KV_F32 ? 4 : 2) / 8;
+    return decode_waves(kind) * 32 * head_dim * (kind == KV_F32 ? 4 : 2) / 8;
 }
 
 struct ReduceParams {
@@ -98,7 +102,7 @@ inline void launch_marked(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipSt
         hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
 }
 
-// paged_decode for one storage kind: grid (max_parts, H / qg, batch), kDecodeWaves waves per
+// paged_decode for one storage kind: grid (max_parts, H / qg, batch), decode_waves(kind) waves per
 // workgroup. `fast`: every 16-token tile lies inside one page (page_size % 16 == 0 and
 // part_tokens % 16 == 0), so block ids and scales are read once per tile.
 hipError_t launch_paged_decode_f32(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s,

@@ -165,10 +165,10 @@ __device__ __forceinline__ float load_agent(float* p) {
 // (waves_per_eu(2): two waves per SIMD, 8 per CU, keep two tiles per wave in flight; the register
 // budget that leaves is 256 per lane)
 template <int KIND, int D, int QG, bool FAST>
-__global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(DecodeParams p) {
     using T = KvT<KIND, D>;
     using R = TileRegs<KIND, D>;
-    constexpr int W = kDecodeWaves;
+    constexpr int W = decode_waves(KIND);
     constexpr int NJ = T::NJ, VL = T::VL, NV = T::NV, NMB = D / 16;
     constexpr bool F32 = KIND == KV_F32;
     static_assert(QG == 1 || QG == 2 || QG == 4 || QG == 8, "QG must be 1, 2, 4 or 8");
@@ -599,7 +599,7 @@ __global__ __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_
 template <int KIND, int D, int QG, bool FAST>
 hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
     const dim3 grid(p.max_parts, p.num_heads / QG, batch);
-    launch_marked(paged_decode_kernel<KIND, D, QG, FAST>, grid, dim3(64 * kDecodeWaves), s, m, p);
+    launch_marked(paged_decode_kernel<KIND, D, QG, FAST>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
     return hipGetLastError();
 }
 

@@ -245,10 +245,11 @@ def test_fused_merge_reads_fresh_partitions(gpu):
         dev.free()
 
 
-@pytest.mark.parametrize("kv,part", [("f16", 16), ("f16", 32), ("f32", 16)])
+@pytest.mark.parametrize("kv,part", [("f16", 16), ("f16", 32), ("f16", 64), ("f32", 16), ("i8", 16), ("i8", 32)])
 def test_many_partitions(gpu, oracle, kv, part):
-    """Partition counts at and past what the fused merge stages in LDS (head group x partitions >
-    fused_merge_slots: the runtime then merges with paged_reduce as a second kernel)."""
+    """Partition counts at and past what the fused merge stages in LDS: at head_dim 64 and 8 heads
+    per group, f16 part 64 (64 partitions) and i8 part 32 (128) fill it exactly; the others exceed
+    it and the runtime merges with paged_reduce as a second kernel."""
     kvb = gpu
     w = kvb.Workload(kvb.Shape(2, 16, 2, 64), kv, [4096, 2049], seed=91)
     c = kvb.PagedCache(w, 16, 91, pool_factor=1.25)

@@ -70,10 +70,10 @@ def test_poison_marks_every_unowned_element(kvb):
 
 
 def test_mi355x_partition_policy(kvb):
-    # c4 (B 4, 64/8 heads, 32k): 4 * 8 workgroups per partition -> 256 at part 4096 (fp16 target),
-    # 512 at part 2048 (int8 target).
+    # c4 (B 4, 64/8 heads, 32k): 4 * 8 workgroups per partition -> 256 at part 4096
     assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768) == 4096
-    assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768, min_groups=kvb.mi355x_min_groups(kvb.KV_I8)) == 2048
+    assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768, min_groups=kvb.mi355x_min_groups(kvb.KV_I8)) == 4096
+    assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768, min_groups=512) == 2048
     assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768, min_groups=1024) == 1024
     # short or small: the floor
     assert kvb.mi355x_part_tokens(kvb.Shape(1, 32, 8, 128), 512) == 256
