@@ -102,7 +102,7 @@ inline void launch_marked(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipSt
         hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
 }
 
-// paged_decode for one storage kind: grid (max_parts, H / qg, batch), decode_waves(kind) waves per
+// paged_decode for one storage kind: grid (H / qg, batch, max_parts), decode_waves(kind) waves per
 // workgroup. `fast`: every 16-token tile lies inside one page (page_size % 16 == 0 and
 // part_tokens % 16 == 0), so block ids and scales are read once per tile.
 hipError_t launch_paged_decode_f32(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s,

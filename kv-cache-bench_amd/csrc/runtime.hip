@@ -146,6 +146,9 @@ int validate_paged(const kvb_paged_args* a) {
     if (int st = check_lens(a->batch, a->host_seq_lens, a->max_len, (size_t)a->max_blocks * (size_t)a->page_size)) return st;
     if (a->batch > 0 && (!a->q || !a->k || !a->v || !a->seq_lens || !a->out || (a->max_blocks > 0 && !a->block_table)))
         return fail(KVB_EINVAL, "null device pointer");
+    // launch grid (H / qg, batch, max_parts): y and z are at most 65535
+    if (a->batch > 65535) return fail(KVB_EINVAL, "batch > 65535");
+    if (max_parts_of(a) > 65535) return fail(KVB_EINVAL, "more than 65535 partitions: part_tokens too small for max_len");
     if (a->workspace && a->workspace_bytes < workspace_need(a))
         return fail(KVB_EINVAL, "workspace smaller than kvb_paged_workspace_bytes()");
     return KVB_OK;

@@ -113,7 +113,9 @@ class TestRefusals:
                                     dict(max_len=-1), dict(page_size=0), dict(part_tokens=-1), dict(head_dim=96),
                                     dict(num_heads=6, num_kv_heads=4), dict(kv_type=2), dict(kv_type=7),
                                     dict(max_blocks=-1), dict(host_seq_lens=None), dict(q=None), dict(out=None),
-                                    dict(workspace=0x1000, workspace_bytes=16)])
+                                    dict(workspace=0x1000, workspace_bytes=16),
+                                    # launch-grid limits (y = batch, z = partitions <= 65535)
+                                    dict(part_tokens=1, max_len=70000), dict(lens=[0] * 65536, batch=65536)])
     def test_refused(self, kvb, kw):
         a = self.args(kvb, **kw)
         assert self.status(kvb, a) == kvb.KVB_EINVAL, kvb.hip.kvb_last_error()
