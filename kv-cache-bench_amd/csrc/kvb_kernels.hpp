@@ -56,10 +56,10 @@ __device__ __forceinline__ float partition_weight(float m, float l, float M) {
 }
 
 // Partition (m, l) pairs the fused merge stages in LDS (the V-tile space of one workgroup: 32
-// tokens x head_dim per wave, fp32 for f32 caches, fp16 otherwise). Past this the partitions are
-// merged by paged_reduce as a second kernel.
+// tokens x head_dim per wave in the storage type). Past this the partitions are merged by
+// paged_reduce as a second kernel.
 constexpr int fused_merge_slots(int kind, int head_dim) {
-    return decode_waves(kind) * 32 * head_dim * (kind == KV_F32 ? 4 : 2) / 8;
+    return decode_waves(kind) * 32 * head_dim * (kind == KV_F32 ? 4 : kind == KV_I8 ? 1 : 2) / 8;
 }
 
 struct ReduceParams {

@@ -47,6 +47,11 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __fp16 fp16x8_t __attribute__((__vector_size__(8 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4_t;
+typedef __attribute__((address_space(3))) i32x2_t lds_i32x2_t;
 
 // Pointers into the constant address space (4): loads through them may be scalar (s_load).
 typedef __attribute__((address_space(4))) const int32_t* const_i32;
@@ -107,8 +112,16 @@ __device__ __forceinline__ half8_t i8x8_to_half8(uint32_t w0, uint32_t w1) {
 // ---- per storage type --------------------------------------------------------------------------
 // KLOADS: 16-byte K loads per lane per half tile; NJ: score MFMAs per half tile; kdoff/dslot: the d
 // order of the score contraction (a K load's first element, and MFMA j slot s). V is read row-major:
-// VL lanes per row (16 bytes each), 64/VL rows per load, NV loads per half tile. In LDS, V is fp16
-// (fp32 for fp32 caches) with row stride D elements; chunk ch of row t sits at ch ^ swz(t).
+// VL lanes per row (16 bytes each), 64/VL rows per load, NV loads per half tile. In LDS, V keeps its
+// storage type (fp16, int8 or fp32) with row stride D elements; 16-byte chunk ch of row t sits at
+// ch ^ vswz(t) (fp32: ch ^ swz(t)).
+//
+// fp16 and int8 V^T operands come from transposing LDS reads (ds_read_b64_tr_b16 / _tr_b8): in each
+// 16-lane group, the 4 halves (8 bytes) that lane l addresses form a flat sequence F, and lane i
+// receives F[i], F[i + 16], ... So for d = 16 mb + i and the lane's 8 tokens, lane l addresses
+// token (l >> 2) [b16] or (l >> 1) [b8] of the 8, at d = 16 mb + 4 (l & 3) [b16] or 8 (l & 1) [b8].
+// vswz spreads the rows one half-wave reads (8 rows x 32 bytes for fp16, 16 x 16 for int8) over
+// all 64 banks.
 
 template <int KIND, int D>
 struct KvT;
@@ -120,16 +133,21 @@ struct KvT<KV_F16, D> {
     static constexpr int LDS_ESZ = 2;
     __device__ static int kdoff(int c, int q4) { return 32 * c + 8 * q4; }
     __device__ static int dslot(int j, int q4, int s) { return 32 * j + 8 * q4 + s; }
-    __device__ static int swz(int t) { return 2 * ((t >> 2) & 3); }
+    // rows 0-7 (and 8-15, 16-23, 24-31): 32-byte chunk pairs at 8 distinct offsets mod 256 bytes
+    __device__ static int vswz(int t) { return D == 128 ? 2 * (t & 7) : 2 * ((t >> 1) & 3); }
 };
 template <int D>
 struct KvT<KV_I8, D> {
     static constexpr int ESZ = 1, KLOADS = D / 64, NJ = D / 32;
     static constexpr int VL = D / 16, NV = kHalf * VL / 64;
-    static constexpr int LDS_ESZ = 2;
+    static constexpr int LDS_ESZ = 1;
     __device__ static int kdoff(int c, int q4) { return 64 * c + 16 * q4; }
     __device__ static int dslot(int j, int q4, int s) { return 64 * (j >> 1) + 16 * q4 + 8 * (j & 1) + s; }
-    __device__ static int swz(int t) { return 2 * ((t >> 2) & 3); }
+    // a half-wave reads rows {0-3, 4-7, 16-19, 20-23} (or the other 16): 16 chunks at distinct
+    // offsets mod 256 bytes
+    __device__ static int vswz(int t) {
+        return D == 128 ? (((t >> 1) & 3) | ((t >> 2) & 4)) : (((t >> 2) & 1) | ((t >> 3) & 2));
+    }
 };
 template <int D>
 struct KvT<KV_F32, D> {
@@ -338,20 +356,17 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     float vdown = 1.0f;
     int ve = -160;
 
-    // ---- V tile -> LDS (row-major, swizzled 16-byte chunks; int8 widened to fp16)
+    // ---- V tile -> LDS as stored (row-major, swizzled 16-byte chunks; int8 is widened to fp16 only
+    // after the transposing read)
     auto store_v = [&](const R& r) {
         for (int h = 0; h < 2; ++h)
             for (int i = 0; i < NV; ++i) {
                 const int t = h * kHalf + i * (64 / VL) + lane / VL;  // tile row
                 const int ch = lane % VL;                             // 16-byte chunk of the loaded row
-                if constexpr (KIND == KV_I8) {
-                    const half8_t a = i8x8_to_half8(r.v[h][i].x, r.v[h][i].y);
-                    const half8_t bb = i8x8_to_half8(r.v[h][i].z, r.v[h][i].w);
-                    *reinterpret_cast<u32x4_t*>(vt + t * D * 2 + 16 * ((2 * ch) ^ T::swz(t))) = __builtin_bit_cast(u32x4_t, a);
-                    *reinterpret_cast<u32x4_t*>(vt + t * D * 2 + 16 * ((2 * ch + 1) ^ T::swz(t))) = __builtin_bit_cast(u32x4_t, bb);
-                } else {
-                    *reinterpret_cast<u32x4_t*>(vt + t * D * T::LDS_ESZ + 16 * (ch ^ T::swz(t))) = __builtin_bit_cast(u32x4_t, r.v[h][i]);
-                }
+                int sch;
+                if constexpr (F32) sch = ch ^ T::swz(t);
+                else sch = ch ^ T::vswz(t);
+                *reinterpret_cast<u32x4_t*>(vt + t * D * T::LDS_ESZ + 16 * sch) = __builtin_bit_cast(u32x4_t, r.v[h][i]);
             }
     };
 
@@ -455,13 +470,21 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                     const float a = *reinterpret_cast<const float*>(vt + t * D * 4 + 16 * ((d >> 2) ^ T::swz(t)) + 4 * (d & 3));
                     acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, pb32[u], acc[mb], 0, 0, 0);
                 }
-            } else {
-                half8_t a;
-                for (int j = 0; j < 8; ++j) {
-                    const int t = 16 * (j >> 2) + 4 * q4 + (j & 3);
-                    a[j] = *reinterpret_cast<const _Float16*>(vt + t * D * 2 + 16 * ((d >> 3) ^ T::swz(t)) + 2 * (d & 7));
-                }
+            } else if constexpr (KIND == KV_F16) {
+                // two reads: tokens 4 q4 + k, then 16 + 4 q4 + k (k < 4), of column d
+                const int t0 = 4 * q4 + (c >> 2), t1 = 16 + t0, ch = (16 * mb + 4 * (c & 3)) >> 3, off = 8 * (c & 1);
+                const fp16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                    (lds_fp16x4_t*)(vt + t0 * D * 2 + 16 * (ch ^ T::vswz(t0)) + off));
+                const fp16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                    (lds_fp16x4_t*)(vt + t1 * D * 2 + 16 * (ch ^ T::vswz(t1)) + off));
+                const half8_t a = __builtin_bit_cast(half8_t, (fp16x8_t){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
                 acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb16, acc[mb], 0, 0, 0);
+            } else {
+                // one read: the 8 tokens of column d as bytes, widened to exact fp16
+                const int k = c >> 1, t = (k < 4 ? 0 : 12) + 4 * q4 + k;
+                const i32x2_t x = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                    (lds_i32x2_t*)(vt + t * D + 16 * (mb ^ T::vswz(t)) + 8 * (c & 1)));
+                acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(x[0], x[1]), pb16, acc[mb], 0, 0, 0);
             }
         }
         // the next store_v overwrites the tile: keep it after these reads
