@@ -139,6 +139,17 @@ def main():
         print("bench.py: no GPU", file=sys.stderr)
         sys.exit(1)
     log(f"device: {kvb.device_name()}")
+    # The probe runs first, and nothing is freed until every GPU measurement is done: on these boxes
+    # kernels run measurably slower for a while after a large hipFree (the same 4 GiB buffer read
+    # 7.05 TB/s before and 6.7 TB/s after other buffers were freed).
+    keep = []
+    if not args.no_extras:
+        probe = kvb.Buffer(4 << 30)
+        probe.fill(1)
+        kvb.run_read_bandwidth(probe)
+        pt = [kvb.run_read_bandwidth(probe) for _ in range(5)]
+        probe_gbps = round((4 << 30) / (statistics.median(pt) * 1e-3) / 1e9, 1)
+        keep.append(probe)
     t_setup = time.perf_counter()
     w, c, cfg = kvb.make_config(args.config, threads=16)
     part = kvb.config_part(cfg, w) if args.part is None else args.part
@@ -171,9 +182,9 @@ def main():
         extras["unfused_reduce_us"] = round(ur * 1e3, 2)
         extras["warm_chain_us"] = round(warm_chain(kvb, dev, part) * 1e3, 2)
         extras["warm_gbps"] = round(bytes_step / (extras["warm_chain_us"] * 1e-6) / 1e9, 1)
+    keep.append(dev)
     if not args.no_extras and args.config == "c4":
         # the same shape with an int8 cache (per-(page, KV head) scales): the int8 / fp16 speed ratio
-        dev.free()
         s = w.shape
         wi = kvb.Workload(s, "i8", list(w.lens), seed=32768, q_amp=1.0, dist="normal", threads=16)
         ci = kvb.PagedCache(wi, 128, 32768 * 131 + 128, pool_factor=1.25, poison=False)
@@ -186,19 +197,13 @@ def main():
         extras["int8_us_per_step"] = round(medi * 1e3, 2)
         extras["int8_gbps"] = round(wi.min_bytes() / (medi * 1e-3) / 1e9, 1)
         extras["int8_speedup_vs_fp16"] = round(med / medi, 3)
-        devi.free()
+        keep.append(devi)
         log(f"int8 c4-shape: {medi * 1e3:.1f} us ({extras['int8_speedup_vs_fp16']}x fp16)")
-    else:
-        dev.free()
     if not args.no_extras:
-        # the streaming-read ceiling, last: its 4 GiB buffer is freed before nothing else is allocated
-        probe = kvb.Buffer(4 << 30)
-        probe.fill(1)
-        kvb.run_read_bandwidth(probe)
-        pt = [kvb.run_read_bandwidth(probe) for _ in range(5)]
-        extras["probe_gbps"] = round((4 << 30) / (statistics.median(pt) * 1e-3) / 1e9, 1)
-        extras["pct_of_probe"] = round(100 * value / extras["probe_gbps"], 1)
-        probe.free()
+        extras["probe_gbps"] = probe_gbps  # the streaming-read ceiling, measured first
+        extras["pct_of_probe"] = round(100 * value / probe_gbps, 1)
+    for x in keep:
+        x.free()
 
     cpu = None
     if not args.no_cpu:
