@@ -107,6 +107,24 @@ struct NaiveArgs {
     const Buffer* out;
 };
 
+// The paged cache written on the GPU from a contiguous cache in HBM: scatter_to_paged for f32/f16
+// and quantize_to_paged_i8 for i8 (fp32 input; scales required), the reference's host-side writers
+// (src/reference.hpp:60-68, src/reference.cpp:32-51) with the same bytes and scales. Only live
+// tokens are written.
+struct CacheWriteArgs {
+    Shape shape;                 // batch, num_kv_heads, head_dim (64 or 128); num_heads is unused
+    KvType type = KvType::f32;
+    int page_size = 16;
+    int max_blocks = 0;
+    int max_len = 0;             // row stride of the contiguous cache
+    const Buffer* contig;        // type [B][Hkv][max_len][D] (fp32 for i8)
+    const Buffer* paged;         // type [blocks][Hkv][page][D]
+    const Buffer* scales = nullptr;  // float [blocks][Hkv], i8 only
+    const Buffer* block_table;   // int32 [B][max_blocks]
+    const Buffer* seq_lens;      // int32 [B]
+};
+double write_paged(const CacheWriteArgs&);
+
 // Each call queues the kernels on one stream, waits, and returns their GPU time in milliseconds,
 // from the first kernel's start to the last kernel's end (events stamped by the dispatches). Throws std::invalid_argument, before any GPU work, for a sequence length below
 // 0, above max_len, or (paged) above max_blocks * page_size, and for the other refusals of

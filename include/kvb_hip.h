@@ -113,6 +113,35 @@ int kvb_run_paged_steps(const kvb_paged_args* a, int steps, double* ms);
  * reference (its timing is per command buffer, src/metal_attn.mm:119-130). */
 int kvb_run_paged_split(const kvb_paged_args* a, double* decode_ms, double* reduce_ms);
 
+/* ---- cache writers on the GPU --------------------------------------------------------------
+ * The producers of the paged cache the decode reads, as the reference runs them on the host:
+ * scatter_to_paged (src/reference.hpp:60-68) for F32/F16 and quantize_to_paged_i8
+ * (src/reference.cpp:32-51) for I8, with the same bytes and scales. Only live tokens' rows (and,
+ * for I8, the scales of live (block, KV head) pairs) are written; the rest of the pool is left as
+ * it was. */
+typedef struct kvb_cache_args {
+    int batch;        /* B */
+    int num_kv_heads; /* Hkv */
+    int head_dim;     /* D: 64 or 128 */
+    int kv_type;      /* KVB_KV_F32 / KVB_KV_F16: copy; KVB_KV_I8: quantise fp32 input */
+    int page_size;
+    int max_blocks;   /* row stride of block_table */
+    int max_len;      /* row stride (in tokens) of the contiguous cache */
+    const void* contig;          /* device, [B][Hkv][max_len][D]: kv_type values, fp32 for I8 */
+    void* paged;                 /* device, [blocks][Hkv][page_size][D] of kv_type */
+    float* scales;               /* device, float [blocks][Hkv]; required for I8 */
+    const int32_t* block_table;  /* device, int32 [B][max_blocks] */
+    const int32_t* seq_lens;     /* device, int32 [B] */
+    const int32_t* host_seq_lens;/* host copy of seq_lens, read by the capacity check */
+} kvb_cache_args;
+
+/* Writes the paged cache; *ms = the kernel's GPU time (0 in pipelined mode). Refuses (KVB_EINVAL,
+ * before any GPU work) bad sizes, head_dim not 64/128, a length < 0 or > max_len or
+ * > max_blocks * page_size, I8 without scales, null device pointers. */
+int kvb_write_paged(const kvb_cache_args* a, double* ms);
+/* The refusals of kvb_write_paged alone; needs no GPU. */
+int kvb_check_write_paged(const kvb_cache_args* a);
+
 /* ---- naive 3-pass baseline (NaiveArgs / run_naive, src/metal_attn.hpp:71-87) ------------- */
 typedef struct kvb_naive_args {
     int batch, num_heads, num_kv_heads, head_dim;

@@ -59,8 +59,17 @@ class NaiveArgsC(ctypes.Structure):
                [(n, _p) for n in ("q", "k", "v", "seq_lens", "host_seq_lens", "out")]
 
 
+class CacheArgsC(ctypes.Structure):
+    """struct kvb_cache_args (include/kvb_hip.h)."""
+
+    _fields_ = [(n, _i) for n in ("batch", "num_kv_heads", "head_dim", "kv_type", "page_size", "max_blocks",
+                                  "max_len")] + \
+               [(n, _p) for n in ("contig", "paged", "scales", "block_table", "seq_lens", "host_seq_lens")]
+
+
 _PA = ctypes.POINTER(PagedArgsC)
 _NA = ctypes.POINTER(NaiveArgsC)
+_CA = ctypes.POINTER(CacheArgsC)
 _SIGS = {
     "kvb_gpu_available": ([], _i),
     "kvb_device_name": ([ctypes.c_char_p, _sz], _i),
@@ -86,6 +95,8 @@ _SIGS = {
     "kvb_end_pipelined": ([_d, _sz, ctypes.POINTER(_sz)], _i),
     "kvb_run_read_bandwidth": ([_p, _sz, _d], _i),
     "kvb_flush_gpu_caches": ([], _i),
+    "kvb_write_paged": ([_CA, _d], _i),
+    "kvb_check_write_paged": ([_CA], _i),
 }
 for _name, (_args, _ret) in _SIGS.items():
     _f = getattr(hip, _name)
@@ -411,6 +422,25 @@ def run_naive(w: Workload, out: Buffer, q: Buffer, k: Buffer, v: Buffer, lens: B
     a.host_seq_lens = host_lens.ctypes.data
     ms = ctypes.c_double()
     check(hip.kvb_run_naive(ctypes.byref(a), ctypes.byref(ms)), "run_naive")
+    return ms.value
+
+
+def write_paged(w: Workload, c: PagedCache, contig: Buffer, paged: Buffer, table: Buffer, lens: Buffer,
+                scales: Buffer | None = None) -> float:
+    """Writes the paged pool (and int8 scales) on the GPU from the contiguous cache in HBM:
+    scatter_to_paged for f32/f16 (src/reference.hpp:60-68), quantize_to_paged_i8 for i8 with fp32
+    input (src/reference.cpp:32-51). c supplies the layout (page, block table); only live rows are
+    written. Returns the kernel's GPU ms."""
+    s = w.shape
+    a = CacheArgsC()
+    a.batch, a.num_kv_heads, a.head_dim, a.kv_type = s.batch, s.num_kv_heads, s.head_dim, w.kv_type
+    a.page_size, a.max_blocks, a.max_len = c.page_size, c.max_blocks, w.max_len
+    a.contig, a.paged, a.block_table, a.seq_lens = contig.ptr, paged.ptr, table.ptr, lens.ptr
+    a.scales = scales.ptr if scales is not None else None
+    host_lens = np.ascontiguousarray(w.lens)
+    a.host_seq_lens = host_lens.ctypes.data
+    ms = ctypes.c_double()
+    check(hip.kvb_write_paged(ctypes.byref(a), ctypes.byref(ms)), "write_paged")
     return ms.value
 
 

@@ -119,6 +119,25 @@ hipError_t launch_paged_reduce(int head_dim, const ReduceParams& p, int batch, h
 hipError_t launch_naive(int kind, int head_dim, int group, const NaiveParams& p, int batch, hipStream_t s,
                         const Marks& m = {});
 
+// The cache writers (scatter_to_paged / quantize_to_paged_i8 on the GPU).
+struct CacheWriteParams {
+    const void* contig;         // [B][Hkv][max_len][D]: elem_size bytes per value, fp32 if quantize
+    void* paged;                // [blocks][Hkv][page][D]: elem_size bytes, int8 if quantize
+    float* scales;              // [blocks][Hkv], quantize only
+    const int32_t* block_table; // [B][max_blocks]
+    const int32_t* seq_lens;    // [B]
+    int num_kv_heads;
+    int head_dim;               // 64 or 128
+    int elem_size;              // 1, 2 or 4 (scatter)
+    int page_size;
+    int max_blocks;
+    int max_len;
+    int quantize;               // 1: fp32 -> int8 with per-(block, KV head) scales
+};
+// grid (Hkv, batch, max_blocks_used): max_blocks_used = ceil(max_len / page)
+hipError_t launch_write_paged(const CacheWriteParams& p, int batch, int max_blocks_used, hipStream_t s,
+                              const Marks& m = {});
+
 // Streaming read of n16 16-byte words over kReadBwGroups workgroups; the guarded store into sink
 // (kReadBwSink floats) never fires for real data.
 constexpr int kReadBwGroups = 32768;

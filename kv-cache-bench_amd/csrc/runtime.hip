@@ -382,6 +382,50 @@ int kvb_run_paged_split(const kvb_paged_args* a, double* decode_ms, double* redu
     return KVB_OK;
 }
 
+int kvb_check_write_paged(const kvb_cache_args* a) {
+    if (!a) return fail(KVB_EINVAL, "null arguments");
+    if (a->kv_type < KVB_KV_F32 || a->kv_type > KVB_KV_I8) return fail(KVB_EINVAL, "unknown kv_type");
+    if (a->batch < 0 || a->num_kv_heads <= 0) return fail(KVB_EINVAL, "batch < 0 or num_kv_heads <= 0");
+    if (a->head_dim != 64 && a->head_dim != 128) return fail(KVB_EINVAL, "head_dim must be 64 or 128");
+    if (a->page_size <= 0 || a->max_blocks < 0 || a->max_len < 0)
+        return fail(KVB_EINVAL, "page_size <= 0, max_blocks < 0 or max_len < 0");
+    if (a->batch > 65535 || ((long long)a->max_len + a->page_size - 1) / a->page_size > 65535)
+        return fail(KVB_EINVAL, "more than 65535 sequences or logical blocks");
+    if (a->batch > 0 && !a->host_seq_lens) return fail(KVB_EINVAL, "host_seq_lens is required");
+    if (int st = check_lens(a->batch, a->host_seq_lens, a->max_len, (size_t)a->max_blocks * (size_t)a->page_size)) return st;
+    if (a->batch > 0 && a->max_len > 0 &&
+        (!a->contig || !a->paged || !a->block_table || !a->seq_lens || (a->kv_type == KVB_KV_I8 && !a->scales)))
+        return fail(KVB_EINVAL, "null device pointer");
+    return KVB_OK;
+}
+
+int kvb_write_paged(const kvb_cache_args* a, double* ms) {
+    if (ms) *ms = 0.0;
+    if (int st = kvb_check_write_paged(a)) return st;
+    if (int st = ensure_device()) return st;
+    if (a->batch == 0 || a->max_len == 0) return KVB_OK;
+    kvbk::CacheWriteParams p{};
+    p.contig = a->contig;
+    p.paged = a->paged;
+    p.scales = a->scales;
+    p.block_table = a->block_table;
+    p.seq_lens = a->seq_lens;
+    p.num_kv_heads = a->num_kv_heads;
+    p.head_dim = a->head_dim;
+    p.elem_size = a->kv_type == KVB_KV_F32 ? 4 : a->kv_type == KVB_KV_F16 ? 2 : 1;
+    p.page_size = a->page_size;
+    p.max_blocks = a->max_blocks;
+    p.max_len = a->max_len;
+    p.quantize = a->kv_type == KVB_KV_I8;
+    hipEvent_t e0, e1;
+    if (int st = get_event(&e0)) return st;
+    if (int st = get_event(&e1)) return st;
+    const int used = (a->max_len + a->page_size - 1) / a->page_size;
+    const hipError_t e = kvbk::launch_write_paged(p, a->batch, used, g.stream, {e0, e1});
+    if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("write_paged launch: ") + hipGetErrorString(e));
+    return finish(e0, e1, ms);
+}
+
 int kvb_check_naive(const kvb_naive_args* a) {
     if (!a) return fail(KVB_EINVAL, "null arguments");
     if (a->kv_type == KVB_KV_I8) return fail(KVB_EINVAL, "naive kernels take f32 or f16 caches");

@@ -177,6 +177,32 @@ double run_naive(const NaiveArgs& a) {
     return ms;
 }
 
+double write_paged(const CacheWriteArgs& a) {
+    kvb_cache_args c{};
+    c.batch = a.shape.batch;
+    c.num_kv_heads = a.shape.num_kv_heads;
+    c.head_dim = a.shape.head_dim;
+    c.kv_type = c_type(a.type);
+    c.page_size = a.page_size;
+    c.max_blocks = a.max_blocks;
+    c.max_len = a.max_len;
+    c.contig = dev(a.contig);
+    c.paged = const_cast<void*>(dev(a.paged));
+    c.scales = static_cast<float*>(const_cast<void*>(dev(a.scales)));
+    c.block_table = static_cast<const int32_t*>(dev(a.block_table));
+    c.seq_lens = static_cast<const int32_t*>(dev(a.seq_lens));
+    c.host_seq_lens = a.seq_lens ? static_cast<const int32_t*>(a.seq_lens->host()) : nullptr;
+    check(kvb_check_write_paged(&c), "write_paged");
+    // the pool (and scales) keep what is not written: bring any host writes over first
+    for (const Buffer* b : {a.contig, a.paged, a.scales, a.block_table, a.seq_lens})
+        if (b) b->device();
+    double ms = 0;
+    check(kvb_write_paged(&c, &ms), "write_paged");
+    a.paged->mark_device_written();
+    if (a.scales) a.scales->mark_device_written();
+    return ms;
+}
+
 void begin_pipelined() { check(kvb_begin_pipelined(), "begin_pipelined"); }
 
 std::vector<double> end_pipelined() {

@@ -140,6 +140,27 @@ class TestRefusals:
         a.kv_type = kvb.KV_I8
         assert kvb.hip.kvb_check_naive(ctypes.byref(a)) == kvb.KVB_EINVAL
 
+    def test_writer_refusals(self, kvb):
+        """kvb_check_write_paged: the cache writer's argument checks, before any GPU work."""
+        lens = np.array([32, 20], np.int32)
+
+        def args(**kw):
+            a = kvb.CacheArgsC()
+            a.batch, a.num_kv_heads, a.head_dim, a.kv_type = 2, 2, 128, kvb.KV_I8
+            a.page_size, a.max_blocks, a.max_len = 16, 2, 32
+            a.host_seq_lens = lens.ctypes.data
+            for name in ("contig", "paged", "scales", "block_table", "seq_lens"):
+                setattr(a, name, 0x1000)
+            for k, v in kw.items():
+                setattr(a, k, v)
+            return kvb.hip.kvb_check_write_paged(ctypes.byref(a))
+
+        assert args() == kvb.KVB_OK
+        assert args(kv_type=kvb.KV_F16, scales=None) == kvb.KVB_OK
+        for kw in (dict(scales=None), dict(head_dim=96), dict(page_size=0), dict(max_len=31), dict(max_blocks=1),
+                   dict(kv_type=5), dict(paged=None), dict(host_seq_lens=None), dict(num_kv_heads=0)):
+            assert args(**kw) == kvb.KVB_EINVAL, kw
+
     def test_valid_without_gpu_is_no_device(self, kvb):
         if kvb.gpu_available():
             pytest.skip("a GPU is present")
