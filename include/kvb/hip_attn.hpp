@@ -131,6 +131,9 @@ double write_paged(const CacheWriteArgs&);
 // kvb_run_paged; std::runtime_error for device failures (src/metal_attn.hpp:82-87).
 double run_paged(const PagedArgs&);
 double run_naive(const NaiveArgs&);
+// The reference's fp64 attention_reference on the GPU (same arguments as run_naive; f32/f16): the
+// accuracy reference of kvbench --accuracy / --dump. Not a fast path.
+double run_attention_fp64(const NaiveArgs&);
 
 // `steps` decode steps on the same inputs, back to back on one stream (src/metal_attn.hpp:89-91).
 double run_paged_steps(const PagedArgs&, int steps);

@@ -159,6 +159,11 @@ typedef struct kvb_naive_args {
 int kvb_run_naive(const kvb_naive_args* a, double* ms);
 /* The refusals of kvb_run_naive alone. */
 int kvb_check_naive(const kvb_naive_args* a);
+/* The reference's fp64 attention_reference (src/reference.cpp:65-100) on the GPU, with the same
+ * arguments as kvb_run_naive: out (fp32) = two-pass fp64 softmax attention over the contiguous
+ * f32 or f16 cache, 0 for an empty sequence. Not a fast path: the accuracy reference of the
+ * benchmark's --accuracy and --dump modes (bench/bench.cpp:130-215). */
+int kvb_run_attention_fp64(const kvb_naive_args* a, double* ms);
 
 /* ---- timing modes (src/metal_attn.hpp:93-99) --------------------------------------------- */
 /* Between begin and end, run_* queue their work without waiting and return 0; end waits and

@@ -90,6 +90,7 @@ _SIGS = {
     "kvb_run_paged_split": ([_PA, _d, _d], _i),
     "kvb_run_naive": ([_NA, _d], _i),
     "kvb_check_naive": ([_NA], _i),
+    "kvb_run_attention_fp64": ([_NA, _d], _i),
     "kvb_begin_pipelined": ([], _i),
     "kvb_pipelined_pending": ([], _sz),
     "kvb_end_pipelined": ([_d, _sz, ctypes.POINTER(_sz)], _i),
@@ -411,7 +412,12 @@ class DeviceCase:
                 b.free()
 
 
-def run_naive(w: Workload, out: Buffer, q: Buffer, k: Buffer, v: Buffer, lens: Buffer) -> float:
+def run_attention_fp64(w: Workload, out: Buffer, q: Buffer, k: Buffer, v: Buffer, lens: Buffer) -> float:
+    """The reference's fp64 attention_reference on the GPU, over the contiguous f32/f16 cache."""
+    return run_naive(w, out, q, k, v, lens, fn="kvb_run_attention_fp64")
+
+
+def run_naive(w: Workload, out: Buffer, q: Buffer, k: Buffer, v: Buffer, lens: Buffer, fn="kvb_run_naive") -> float:
     """The 3-pass baseline over the contiguous cache (src/metal_attn.mm:211-247)."""
     s = w.shape
     a = NaiveArgsC()
@@ -421,7 +427,7 @@ def run_naive(w: Workload, out: Buffer, q: Buffer, k: Buffer, v: Buffer, lens: B
     host_lens = np.ascontiguousarray(w.lens)
     a.host_seq_lens = host_lens.ctypes.data
     ms = ctypes.c_double()
-    check(hip.kvb_run_naive(ctypes.byref(a), ctypes.byref(ms)), "run_naive")
+    check(getattr(hip, fn)(ctypes.byref(a), ctypes.byref(ms)), fn)
     return ms.value
 
 

@@ -3,9 +3,14 @@
 // step; caches are flushed (1 GiB streaming read) before every timed run unless --no-flush; runs are
 // queued back to back (pipelined) unless --sync; the median of --reps runs is reported.
 // --chain=N times N back-to-back steps per submission with warm caches (run_paged_steps).
-// --bw runs the read-bandwidth probe. --config=c1..c5 selects a BASELINE configuration (N(0,1)
-// data, its page, partition and pool). The fp64 CPU leg is timed by bench.py's cpu_baseline.
+// --bw runs the read-bandwidth probe. --config=c1..c4 selects a BASELINE configuration (N(0,1)
+// data, its page, partition and pool). --accuracy instead prints the error of the paged kernel for
+// each storage type against the fp64 attention of the unrounded fp32 data; --dump=DIR writes the
+// inputs and fp64 outputs as raw little-endian fp32 files (the reference's bench/bench.cpp:126-215).
+// The fp64 outputs come from the GPU fp64 reference (run_attention_fp64). The fp64 CPU leg is timed
+// by bench.py's cpu_baseline.
 #include <algorithm>
+#include <cmath>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -48,7 +53,8 @@ int main(int argc, char** argv) {
     std::vector<int> lens{512, 1024, 2048, 4096, 8192, 16384, 32768}, pages{16, 32, 64, 128}, parts{0};
     std::vector<KvType> types{KvType::f32, KvType::f16, KvType::i8};
     int reps = 30, warmup = 3, chain = 0;
-    bool naive = true, flush = true, per_head = false, bw = false, sync = false;
+    bool naive = true, flush = true, per_head = false, bw = false, sync = false, accuracy = false;
+    std::string dump;
     Dist dist = Dist::uniform;
     double pool = 1.0;
     std::string config;
@@ -82,6 +88,8 @@ int main(int argc, char** argv) {
         else if (!std::strcmp(a, "--per-head")) per_head = true;
         else if (!std::strcmp(a, "--bw")) bw = true;
         else if (!std::strcmp(a, "--sync")) sync = true;
+        else if (!std::strcmp(a, "--accuracy")) accuracy = true;
+        else if (auto v = val("--dump")) dump = v;
         else {
             std::fprintf(stderr, "unknown argument %s\n", a);
             return 2;
@@ -131,6 +139,62 @@ int main(int argc, char** argv) {
         const Stats s = time_gpu([&] { return run_read_bandwidth(src); });
         std::printf("read_bw,%zu,%d,%.2f,%.2f,%.2f,%.1f\n", src.size(), reps, s.median * 1e3, s.min * 1e3, s.max * 1e3,
                     double(src.size()) / (s.median * 1e-3) / 1e9);
+        return 0;
+    }
+    // fp64 attention of a workload's contiguous cache (f32/f16 values as stored)
+    auto reference = [&](const Workload& w) {
+        Buffer out(w.out_floats() * sizeof(float));
+        run_attention_fp64(w.naive_args(out));
+        return std::vector<float>(out.as<float>(), out.as<float>() + w.out_floats());
+    };
+    if (!dump.empty()) {  // L<n>_{q,k,v}.f32: q [B][H][D], K, V [B][Hkv][L][D]; L<n>_ref_{f32,f16}.f32: [B][H][D]
+        auto write = [&](const std::string& file, const void* p, size_t bytes) {
+            FILE* f = std::fopen((dump + "/" + file).c_str(), "wb");
+            const bool ok = f && std::fwrite(p, 1, bytes, f) == bytes;
+            if (f) std::fclose(f);
+            if (!ok) {
+                std::fprintf(stderr, "cannot write %s/%s\n", dump.c_str(), file.c_str());
+                std::exit(1);
+            }
+        };
+        for (int L : lens) {
+            const std::string pre = "L" + std::to_string(L) + "_";
+            for (KvType type : {KvType::f32, KvType::f16}) {
+                const Workload w(shape, type, std::vector<int>(size_t(shape.batch), L), uint64_t(L), 3.0f, false, false, dist);
+                const std::vector<float> ref = reference(w);
+                write(pre + "ref_" + name(type) + ".f32", ref.data(), ref.size() * sizeof(float));
+                if (type == KvType::f32) {  // the f16 workload holds these values rounded to fp16
+                    write(pre + "q.f32", w.q->host(), w.q->size());
+                    write(pre + "k.f32", w.k->host(), w.k->size());
+                    write(pre + "v.f32", w.v->host(), w.v->size());
+                }
+            }
+        }
+        return 0;
+    }
+    if (accuracy) {  // same seed = same q and fp32 K/V for every type; f16 rounds them, i8 quantizes per block
+        std::printf("data,dtype,seq_len,page,max_abs_err,rms_err\n");
+        for (bool varied : {false, true})
+            for (int L : lens) {
+                const std::vector<int> ls(size_t(shape.batch), L);
+                const Workload exact(shape, KvType::f32, ls, uint64_t(L), 3.0f, false, varied, dist);
+                const std::vector<float> ref = reference(exact);
+                for (KvType type : types)
+                    for (int page : pages) {
+                        const Workload w(shape, type, ls, uint64_t(L), 3.0f, false, varied, dist);
+                        const PagedCache cache(w, page, uint64_t(L) * 131 + page, false, pool, false);
+                        Buffer out(ref.size() * sizeof(float));
+                        run_paged(cache.args(w, parts[0], out));
+                        double mx = 0, sq = 0;
+                        for (size_t i = 0; i < ref.size(); ++i) {
+                            const double e = std::fabs(double(out.as<float>()[i]) - ref[i]);
+                            mx = std::max(mx, e), sq += e * e;
+                        }
+                        std::printf("%s,%s,%d,%d,%.3g,%.3g\n", varied ? "varied" : "uniform", name(type), L, page, mx,
+                                    std::sqrt(sq / double(ref.size())));
+                        std::fflush(stdout);
+                    }
+            }
         return 0;
     }
     if (chain) {  // warm, back-to-back steps in one submission

@@ -94,6 +94,64 @@ __global__ void naive_pv_kernel(NaiveParams p, int D, int G) {
     p.out[((size_t)b * H + h) * D + d] = o;
 }
 
+// fp64 attention over the contiguous cache, one workgroup per (h, b): the reference's
+// attention_reference (src/reference.cpp:65-100) on the GPU, for the bench's accuracy and dump
+// modes. Two passes over the tokens, as there: the max score, then exp(s - max) summed with the
+// weighted V rows; out = acc / sum, 0 for an empty sequence. Scores are recomputed in the second
+// pass instead of stored.
+__device__ double block_reduce_double(double x, bool is_max) {
+    for (int o = 32; o > 0; o >>= 1) {
+        const double y = __shfl_xor(x, o);
+        x = is_max ? fmax(x, y) : x + y;
+    }
+    __shared__ double s_red[4];
+    __syncthreads();  // s_red may still be read from the previous call
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = x;
+    __syncthreads();
+    double r = s_red[0];
+    for (int w = 1; w < 4; ++w) r = is_max ? fmax(r, s_red[w]) : r + s_red[w];
+    return r;
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void attention_fp64_kernel(NaiveParams p, int D, int G) {
+    const int h = blockIdx.x, b = blockIdx.y, H = p.num_heads, len = p.seq_lens[b], tid = threadIdx.x;
+    const size_t kv0 = ((size_t)b * p.num_kv_heads + h / G) * p.max_len * D;
+    const double scale = p.scale;  // the reference's float 1/sqrt(D), widened
+    __shared__ double s_q[128];
+    __shared__ double s_e[256];
+    __shared__ double s_acc[256];
+    for (int d = tid; d < D; d += 256) s_q[d] = p.q[((size_t)b * H + h) * D + d];
+    __syncthreads();
+    auto score = [&](int t) {
+        double s = 0.0;
+        for (int d = 0; d < D; ++d) s += s_q[d] * (double)kv_at<KIND>(p.k, kv0 + (size_t)t * D + d);
+        return s * scale;
+    };
+    double m = -HUGE_VAL;
+    for (int t = tid; t < len; t += 256) m = fmax(m, score(t));
+    m = block_reduce_double(m, true);
+    const int d = tid % D, slices = 256 / D, sl = tid / D;
+    double l = 0.0, acc = 0.0;
+    for (int t0 = 0; t0 < len; t0 += 256) {
+        const double e = t0 + tid < len ? exp(score(t0 + tid) - m) : 0.0;
+        s_e[tid] = e;
+        l += e;
+        __syncthreads();
+        for (int j = sl; j < 256 && t0 + j < len; j += slices)
+            acc += s_e[j] * (double)kv_at<KIND>(p.v, kv0 + (size_t)(t0 + j) * D + d);
+        __syncthreads();
+    }
+    l = block_reduce_double(l, false);
+    s_acc[tid] = acc;
+    __syncthreads();
+    if (tid < D) {
+        double o = 0.0;
+        for (int k = 0; k < slices; ++k) o += s_acc[k * D + tid];
+        p.out[((size_t)b * H + h) * D + tid] = len > 0 ? (float)(o / l) : 0.0f;
+    }
+}
+
 // Grid-stride streaming read with 8 independent 16-byte loads in flight per lane
 // (src/kernels.metal:220-233). XOR-accumulated; the store fires only on a sentinel no real
 // buffer of the probe (all words equal) produces.
@@ -139,6 +197,14 @@ hipError_t launch_naive(int kind, int head_dim, int group, const NaiveParams& p,
     hipLaunchKernelGGL(naive_softmax_kernel, dim3(p.num_heads, batch), dim3(256), 0, s, p);
     if (kind == KV_F16) launch_marked(naive_pv_kernel<KV_F16>, dim3(p.num_heads, batch), dim3(head_dim), s, last, p, head_dim, group);
     else launch_marked(naive_pv_kernel<KV_F32>, dim3(p.num_heads, batch), dim3(head_dim), s, last, p, head_dim, group);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_fp64(int kind, int head_dim, int group, const NaiveParams& p, int batch, hipStream_t s,
+                                 const Marks& m) {
+    const dim3 grid(p.num_heads, batch);
+    if (kind == KV_F16) launch_marked(attention_fp64_kernel<KV_F16>, grid, dim3(256), s, m, p, head_dim, group);
+    else launch_marked(attention_fp64_kernel<KV_F32>, grid, dim3(256), s, m, p, head_dim, group);
     return hipGetLastError();
 }
 

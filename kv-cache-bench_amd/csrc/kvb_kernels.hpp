@@ -138,6 +138,10 @@ struct CacheWriteParams {
 hipError_t launch_write_paged(const CacheWriteParams& p, int batch, int max_blocks_used, hipStream_t s,
                               const Marks& m = {});
 
+// fp64 attention over the contiguous cache (f32 or f16), grid (H, batch): the accuracy reference.
+hipError_t launch_attention_fp64(int kind, int head_dim, int group, const NaiveParams& p, int batch, hipStream_t s,
+                                 const Marks& m = {});
+
 // Streaming read of n16 16-byte words over kReadBwGroups workgroups; the guarded store into sink
 // (kReadBwSink floats) never fires for real data.
 constexpr int kReadBwGroups = 32768;

@@ -457,6 +457,22 @@ int kvb_run_naive(const kvb_naive_args* a, double* ms) {
     return finish(e0, e1, ms);
 }
 
+int kvb_run_attention_fp64(const kvb_naive_args* a, double* ms) {
+    if (ms) *ms = 0.0;
+    if (int st = kvb_check_naive(a)) return st;
+    if (int st = ensure_device()) return st;
+    if (a->batch == 0) return KVB_OK;
+    kvbk::NaiveParams p{a->q, a->k, a->v, a->seq_lens, nullptr, a->out,
+                        a->num_heads, a->num_kv_heads, a->max_len, 1.0f / std::sqrt((float)a->head_dim)};
+    hipEvent_t e0, e1;
+    if (int st = get_event(&e0)) return st;
+    if (int st = get_event(&e1)) return st;
+    const hipError_t e = kvbk::launch_attention_fp64(a->kv_type, a->head_dim, a->num_heads / a->num_kv_heads, p,
+                                                     a->batch, g.stream, {e0, e1});
+    if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("attention_fp64 launch: ") + hipGetErrorString(e));
+    return finish(e0, e1, ms);
+}
+
 int kvb_begin_pipelined(void) {
     if (int st = ensure_device()) return st;
     g.pipelined = true;

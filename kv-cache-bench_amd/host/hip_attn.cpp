@@ -154,6 +154,36 @@ KernelTimes run_paged_split(const PagedArgs& a) {
     return t;
 }
 
+namespace {
+kvb_naive_args naive_view(const NaiveArgs& a) {
+    kvb_naive_args c{};
+    c.batch = a.shape.batch;
+    c.num_heads = a.shape.num_heads;
+    c.num_kv_heads = a.shape.num_kv_heads;
+    c.head_dim = a.shape.head_dim;
+    c.kv_type = c_type(a.type);
+    c.max_len = a.max_len;
+    c.q = static_cast<const float*>(dev(a.q));
+    c.k = dev(a.k);
+    c.v = dev(a.v);
+    c.seq_lens = static_cast<const int32_t*>(dev(a.seq_lens));
+    c.host_seq_lens = a.seq_lens ? static_cast<const int32_t*>(a.seq_lens->host()) : nullptr;
+    c.out = static_cast<float*>(const_cast<void*>(dev(a.out)));
+    return c;
+}
+}  // namespace
+
+double run_attention_fp64(const NaiveArgs& a) {
+    kvb_naive_args c = naive_view(a);
+    check(kvb_check_naive(&c), "run_attention_fp64");
+    for (const Buffer* b : {a.q, a.k, a.v, a.seq_lens, a.out})
+        if (b) b->device();
+    double ms = 0;
+    check(kvb_run_attention_fp64(&c, &ms), "run_attention_fp64");
+    a.out->mark_device_written();
+    return ms;
+}
+
 double run_naive(const NaiveArgs& a) {
     kvb_naive_args c{};
     c.batch = a.shape.batch;

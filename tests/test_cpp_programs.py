@@ -53,3 +53,45 @@ def test_gpu_tests_grid(gpu):
 def test_boundary_tests(gpu):
     rc, out = run("boundary_tests", 900)
     assert rc == 0, out[-4000:]
+
+
+KVBENCH = os.path.join(ROOT, "kv-cache-bench_amd", "build", "kvbench")
+
+
+@pytest.mark.gpu
+def test_kvbench_accuracy(gpu):
+    """--accuracy (the reference's bench/bench.cpp:186-215): one CSV row per (data, type, page); the
+    fp32 cache's error is the kernel's own (<= 2e-5 against fp64 on the same values), fp16 and int8
+    add their storage error."""
+    out = subprocess.run([KVBENCH, "--accuracy", "--batch=2", "--lens=300,1000", "--pages=16,64"],
+                         capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    rows = [r.split(",") for r in out.stdout.splitlines() if r and not r.startswith("#")]
+    assert rows[0] == ["data", "dtype", "seq_len", "page", "max_abs_err", "rms_err"]
+    body = rows[1:]
+    assert len(body) == 2 * 2 * 3 * 2  # data x lens x types x pages
+    for data, dtype, L, page, mx, rms in body:
+        mx, rms = float(mx), float(rms)
+        assert 0 <= rms <= mx
+        assert mx <= {"f32": 2e-5, "f16": 2e-3, "i8": 5e-2}[dtype], (data, dtype, L, page, mx)
+    progress("[kvbench] accuracy: " + "; ".join(f"{d} {t} L{L} p{p}: {m}" for d, t, L, p, m, _ in body[:6]))
+
+
+@pytest.mark.gpu
+def test_kvbench_dump(gpu, oracle, tmp_path):
+    """--dump: raw fp32 inputs and fp64 outputs; the f32 output recomputed by the oracle from the
+    dumped inputs must agree (both are fp64 attention on the same values)."""
+    import numpy as np
+    B, H, Hkv, D, L = 2, 32, 8, 128, 200
+    out = subprocess.run([KVBENCH, f"--dump={tmp_path}", f"--batch={B}", f"--lens={L}"],
+                         capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    q = np.fromfile(tmp_path / f"L{L}_q.f32", np.float32).reshape(B, H, D)
+    k = np.fromfile(tmp_path / f"L{L}_k.f32", np.float32).reshape(B, Hkv, L, D)
+    v = np.fromfile(tmp_path / f"L{L}_v.f32", np.float32).reshape(B, Hkv, L, D)
+    ref32 = np.fromfile(tmp_path / f"L{L}_ref_f32.f32", np.float32).reshape(B, H, D)
+    ref16 = np.fromfile(tmp_path / f"L{L}_ref_f16.f32", np.float32).reshape(B, H, D)
+    want = oracle.attention(gpu.Shape(B, H, Hkv, D), np.array([L] * B, np.int32), L, q, k, v)
+    assert oracle.max_abs_diff(ref32, want) <= 1e-6
+    # the f16 dump is of the fp16-rounded values: close to, not equal to, the fp32 one
+    assert 0 < oracle.max_abs_diff(ref16, ref32) < 1e-2

@@ -201,6 +201,28 @@ def test_naive_matches_oracle(gpu, oracle):
         assert oracle.max_abs_diff(got, want) <= 2e-5
 
 
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+@pytest.mark.parametrize("shape", [(3, 8, 2, 128), (2, 32, 8, 64), (1, 4, 4, 128)])
+def test_attention_fp64_matches_oracle(gpu, oracle, kv, shape):
+    """The GPU fp64 reference (kvbench's accuracy reference) and the oracle are both fp64
+    two-pass attention on the same stored values: they agree to fp32 rounding."""
+    kvb = gpu
+    s = kvb.Shape(*shape)
+    lens = [0, 1, 300, 77][:s.batch] if s.batch > 1 else [513]
+    w = kvb.Workload(s, kv, lens, seed=71, q_amp=3.0)
+    bufs = [kvb.Buffer.from_array(x) for x in (w.q, w.k, w.v, w.lens)]
+    out = kvb.Buffer(w.out_floats() * 4)
+    out.fill(0xFF)
+    kvb.run_attention_fp64(w, out, *bufs)
+    got = out.download(np.float32, w.q.shape)
+    want = oracle.attention(w.shape, w.lens, w.max_len, w.q, w.k, w.v)
+    assert oracle.max_abs_diff(got, want) <= 1e-6
+    for b in np.flatnonzero(w.lens == 0):
+        assert not got[b].any()
+    for x in bufs + [out]:
+        x.free()
+
+
 def test_steps_pipelined_and_deterministic(gpu):
     kvb = gpu
     w = kvb.Workload(kvb.Shape(2, 32, 8, 128), "f16", [4096, 1000], seed=71)
