@@ -17,7 +17,8 @@ from dataclasses import dataclass
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-BUILD = os.path.join(HERE, "build")
+# KVB_BUILD_DIR: libraries built from a mutated copy of the sources (tests/mutation/mutate.py)
+BUILD = os.environ.get("KVB_BUILD_DIR") or os.path.join(HERE, "build")
 
 KVB_OK, KVB_EINVAL, KVB_ERUNTIME, KVB_ENODEV = 0, 1, 2, 3
 KV_F32, KV_F16, KV_I8 = 0, 1, 2

@@ -7,6 +7,7 @@
  */
 #include "kvb_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
@@ -380,4 +381,191 @@ double kvbo_i8_storage_bound(const kvbo_shape* s, const int* lens, int page_size
             }
         }
     return vmax * expm1(2 * E) + vq + 2e-5;
+}
+
+/* ---- CPU model of the split-K decode kernel -------------------------------------------------- */
+
+enum { kModelTile = 16, kModelMaxWaves = 8, kModelMaxD = 128 };
+
+/* The GPU's exp unit returns 0 where the result would be subnormal; the kernel's one-hot and
+ * dominant-key results depend on it. */
+static inline float exp_ftz(float x) {
+    const float e = expf(x);
+    return e < FLT_MIN ? 0.0f : e;
+}
+
+typedef struct {
+    const kvbo_shape* s;
+    int kv_type, page_size, max_blocks;
+    const int32_t* table;
+    const int* lens;
+    const float *q, *k_scale, *v_scale;
+    const void *k, *v;
+    float scale;
+    int part_tokens, max_parts, waves;
+    float *ws_out, *ws_ml, *out; /* workspace [B*H*max_parts + 1 spare][D] and [..][2], NaN-filled */
+    int phase, worker, threads;
+} split_job;
+
+static void load_row(const void* pool, int kv_type, size_t at, int D, float* dst) {
+    for (int d = 0; d < D; ++d) {
+        if (kv_type == 0) dst[d] = ((const float*)pool)[at + d];
+        else if (kv_type == 1) dst[d] = kvbo_f16_to_f32(((const uint16_t*)pool)[at + d]);
+        else dst[d] = (float)((const int8_t*)pool)[at + d];
+    }
+}
+
+/* One partition of one (sequence, query head): the decode kernel's workgroup, one head of its group. */
+static void model_partition(const split_job* j, int b, int h, int part) {
+    const kvbo_shape* s = j->s;
+    const int D = s->head_dim, P = j->page_size, Hkv = s->num_kv_heads;
+    const int kvh = h / (s->num_heads / Hkv);
+    const int len = j->lens[b];
+    const int t0 = part * j->part_tokens;
+    if (t0 >= len) return; /* an empty partition writes nothing */
+    const int t1 = len < t0 + j->part_tokens ? len : t0 + j->part_tokens;
+    const float* qr = j->q + ((size_t)b * s->num_heads + h) * D;
+    const int32_t* bt = j->table + (size_t)b * j->max_blocks;
+    float wm[kModelMaxWaves], wl[kModelMaxWaves], wacc[kModelMaxWaves][kModelMaxD];
+    float krow[kModelMaxD], vrow[kModelTile][kModelMaxD], sc[kModelTile], vs[kModelTile];
+    for (int w = 0; w < j->waves; ++w) {
+        float m = -INFINITY, l = 0.0f;
+        float* acc = wacc[w];
+        for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+        for (int tt = t0 + w * kModelTile; tt < t1; tt += j->waves * kModelTile) {
+            const int n = t1 - tt < kModelTile ? t1 - tt : kModelTile; /* tokens past t1 are masked */
+            float mt = -INFINITY;
+            for (int i = 0; i < n; ++i) {
+                const int t = tt + i;
+                const size_t blk = (size_t)bt[t / P];
+                const size_t row = ((blk * Hkv + kvh) * P + t % P) * D;
+                load_row(j->k, j->kv_type, row, D, krow);
+                load_row(j->v, j->kv_type, row, D, vrow[i]);
+                float dot = 0.0f;
+                for (int d = 0; d < D; ++d) dot += qr[d] * krow[d];
+                sc[i] = dot * j->scale;
+                vs[i] = 1.0f;
+                if (j->kv_type == 2) {
+                    sc[i] *= j->k_scale[blk * Hkv + kvh];
+                    vs[i] = j->v_scale[blk * Hkv + kvh];
+                }
+                if (sc[i] > mt) mt = sc[i];
+            }
+            const float m_new = m > mt ? m : mt;
+            const float corr = exp_ftz(m - m_new); /* rescales the tile-old state to the new max */
+            l *= corr;
+            for (int d = 0; d < D; ++d) acc[d] *= corr;
+            for (int i = 0; i < n; ++i) {
+                const float p = exp_ftz(sc[i] - m_new);
+                l += p;
+                const float pv = p * vs[i];
+                for (int d = 0; d < D; ++d) acc[d] += pv * vrow[i][d];
+            }
+            m = m_new;
+        }
+        wm[w] = m;
+        wl[w] = l;
+    }
+    /* the workgroup's merge of its wave states */
+    float M = -INFINITY, L = 0.0f, wt[kModelMaxWaves];
+    for (int w = 0; w < j->waves; ++w)
+        if (wm[w] > M) M = wm[w];
+    for (int w = 0; w < j->waves; ++w) {
+        wt[w] = exp_ftz(wm[w] - M);
+        L += wl[w] * wt[w];
+    }
+    const size_t slot = ((size_t)b * s->num_heads + h) * j->max_parts + part;
+    for (int d = 0; d < D; ++d) {
+        float o = 0.0f;
+        for (int w = 0; w < j->waves; ++w) o += wacc[w][d] * wt[w];
+        j->ws_out[slot * D + d] = o / L;
+    }
+    j->ws_ml[2 * slot] = M;
+    j->ws_ml[2 * slot + 1] = L;
+}
+
+/* paged_reduce for one (sequence, query head). */
+static void model_reduce(const split_job* j, int b, int h) {
+    const int D = j->s->head_dim;
+    const size_t row = (size_t)b * j->s->num_heads + h;
+    float* out = j->out + row * D;
+    const int parts = (j->lens[b] + j->part_tokens - 1) / j->part_tokens;
+    if (parts == 0) { /* an empty sequence attends to nothing */
+        for (int d = 0; d < D; ++d) out[d] = 0.0f;
+        return;
+    }
+    const float* ml = j->ws_ml + 2 * row * j->max_parts;
+    const float* po = j->ws_out + row * j->max_parts * D;
+    float M = -INFINITY;
+    for (int i = 0; i < parts; ++i)
+        if (ml[2 * i] > M) M = ml[2 * i];
+    for (int d = 0; d < D; ++d) {
+        float L = 0.0f, o = 0.0f;
+        for (int i = 0; i < parts; ++i) {
+            const float w = ml[2 * i + 1] * exp_ftz(ml[2 * i] - M); /* l_i exp(m_i - M) */
+            L += w;
+            o += w * po[(size_t)i * D + d];
+        }
+        out[d] = o / L;
+    }
+}
+
+static void* split_worker(void* arg) {
+    const split_job* j = (const split_job*)arg;
+    const int H = j->s->num_heads, rows = j->s->batch * H;
+    for (int r = j->worker; r < rows; r += j->threads) {
+        if (j->phase == 0)
+            for (int p = 0; p < j->max_parts; ++p) model_partition(j, r / H, r % H, p);
+        else
+            model_reduce(j, r / H, r % H);
+    }
+    return NULL;
+}
+
+int kvbo_split_decode(const kvbo_shape* s, int kv_type, int page_size, int max_blocks, const int32_t* table,
+                      const int* lens, int max_len, const float* q, const void* k_pool, const void* v_pool,
+                      const float* k_scale, const float* v_scale, float scale, int part_tokens, int waves,
+                      float* part_out, float* part_ml, float* out, int threads) {
+    if (!s || s->batch < 0 || s->num_kv_heads <= 0 || s->num_heads % s->num_kv_heads || s->head_dim <= 0 ||
+        s->head_dim > kModelMaxD || kv_type < 0 || kv_type > 2 || page_size <= 0 || max_len < 0 ||
+        part_tokens < 0 || waves < 1 || waves > kModelMaxWaves || (kv_type == 2 && (!k_scale || !v_scale)))
+        return -1;
+    if (part_tokens == 0) part_tokens = kvbo_auto_part_tokens(s->batch, s->num_kv_heads, max_len);
+    const int max_parts = max_len > 0 ? (max_len + part_tokens - 1) / part_tokens : 1;
+    const int D = s->head_dim, rows = s->batch * s->num_heads;
+    const size_t slots = (size_t)rows * max_parts + 1; /* one spare, NaN, past the last row */
+    float* ws_out = (float*)malloc(sizeof(float) * slots * D);
+    float* ws_ml = (float*)malloc(sizeof(float) * slots * 2);
+    if (!ws_out || !ws_ml) {
+        free(ws_out);
+        free(ws_ml);
+        return -1;
+    }
+    for (size_t i = 0; i < slots * D; ++i) ws_out[i] = NAN;
+    for (size_t i = 0; i < slots * 2; ++i) ws_ml[i] = NAN;
+    if (threads < 1) threads = 1;
+    if (rows > 0 && threads > rows) threads = rows;
+    split_job* jobs = (split_job*)malloc(sizeof(split_job) * (size_t)threads);
+    pthread_t* tids = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
+    for (int phase = 0; phase < 2 && rows > 0; ++phase) { /* decode, then merge: two kernels */
+        for (int w = 0; w < threads; ++w) {
+            split_job j = {s, kv_type, page_size, max_blocks, table, lens, q, k_scale, v_scale, k_pool, v_pool,
+                           scale, part_tokens, max_parts, waves, ws_out, ws_ml, out, phase, w, threads};
+            jobs[w] = j;
+        }
+        int started = 0;
+        for (int w = 1; w < threads; ++w)
+            if (pthread_create(&tids[w], NULL, split_worker, &jobs[w]) == 0) started = w;
+            else break;
+        for (int w = started + 1; w < threads; ++w) split_worker(&jobs[w]);
+        split_worker(&jobs[0]);
+        for (int w = 1; w <= started; ++w) pthread_join(tids[w], NULL);
+    }
+    if (part_out) memcpy(part_out, ws_out, sizeof(float) * (slots - 1) * D);
+    if (part_ml) memcpy(part_ml, ws_ml, sizeof(float) * (slots - 1) * 2);
+    free(jobs);
+    free(tids);
+    free(ws_out);
+    free(ws_ml);
+    return max_parts;
 }

@@ -24,6 +24,11 @@
  *   - max_abs_diff: the NaN KAT of tests/boundary_tests.cpp:80-85.
  *   - mt19937_64: the 10000th output fixed by the C++ standard ([rand.predef]).
  *   - f16 conversion: exhaustive agreement with the hardware/compiler conversion in tests.
+ *   - partition_state: the states merge back to attention_f32 (the split-K identity).
+ *   - fp16/int8 storage bounds: sound on constructed cases that need each of their terms (a V
+ *     tie that rounds down; two K rows that round to one stored row from either side).
+ *   - split_decode (a CPU model of this build's kernel): the GPU parity battery, run on it.
+ * tests/mutation/mutate.py plants mistakes in this file and checks that those pins catch each one.
  */
 #ifndef KVB_ORACLE_H
 #define KVB_ORACLE_H
@@ -116,6 +121,26 @@ int kvbo_partition_state_f32(const kvbo_shape* s, const int* lens, int max_len, 
 /* Split-K partition size when part_tokens is 0 (src/metal_attn.hpp:43-51): the largest power of
  * two in [64, 512] with batch * Hkv * ceil(max_len / part) >= 512. */
 int kvbo_auto_part_tokens(int batch, int num_kv_heads, int max_len);
+
+/* A CPU model of this build's split-K decode (kv-cache-bench_amd/csrc/paged_decode_impl.hpp), in
+ * fp32, reading the paged pool through the block table as the kernel does. Per (sequence, query
+ * head) and partition of part_tokens tokens (src/kernels.metal:60-64): `waves` online-softmax
+ * states over tiles of 16 tokens taken round robin (the tail tile masked at the sequence end), the
+ * int8 K scale on the score and the V scale on p; the states merge with weights exp(m_w - M) into
+ * the partition's (o / L, M, L) (src/kernels.metal:97-120). Then, as a second phase, the partition
+ * merge of paged_reduce (src/kernels.metal:124-147): out = sum w_i o_i / sum w_i with
+ * w_i = l_i exp(m_i - M); an empty sequence gives 0. exp is evaluated as the GPU's exp unit
+ * returns it, with results below 2^-126 zero.
+ * kv_type: 0 fp32, 1 fp16 (bit patterns), 2 int8 with k_scale / v_scale [pool blocks][Hkv].
+ * part_tokens 0 means kvbo_auto_part_tokens. part_out [B][H][max_parts][D] and
+ * part_ml [B][H][max_parts][2] may be NULL; the slots of empty partitions are left NaN.
+ * Returns max_parts, or -1 on bad arguments.
+ * It is the host of the mutation harness's planted kernel mistakes (tests/mutation/mutate.py), and
+ * it is pinned by the same parity battery as the GPU kernels (tests/test_split_model.py). */
+int kvbo_split_decode(const kvbo_shape* s, int kv_type, int page_size, int max_blocks, const int32_t* table,
+                      const int* lens, int max_len, const float* q, const void* k_pool, const void* v_pool,
+                      const float* k_scale, const float* v_scale, float scale, int part_tokens, int waves,
+                      float* part_out, float* part_ml, float* out, int threads);
 
 /* Derived storage-error bounds (tests/gpu_tests.cpp:16-62). q is [B][H][D] fp32; k32/v32 the
  * unrounded fp32 contiguous data; scales [pool][Hkv]. Both include the 2e-5 kernel tolerance. */

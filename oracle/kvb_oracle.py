@@ -11,7 +11,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB = os.path.join(HERE, "build", "libkvb_oracle.so")
+# KVBO_LIB: a build of a mutated copy of kvb_oracle.c (tests/mutation/mutate.py); unset, the in-tree build
+LIB = os.environ.get("KVBO_LIB") or os.path.join(HERE, "build", "libkvb_oracle.so")
 REF = os.path.join(HERE, "_ref", "libkvbref.so")
 
 _p, _i, _sz, _dbl = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_double
@@ -39,6 +40,7 @@ for name, args, ret in [
     ("kvbo_attention_f16", [_SP, _p, _i, _p, _p, _p, _p, ctypes.c_float, _i], None),
     ("kvbo_partition_state_f32", [_SP, _p, _i, _p, _p, _p, ctypes.c_float, _i, _i, _i, _i, _p, _p, _p], _i),
     ("kvbo_auto_part_tokens", [_i, _i, _i], _i),
+    ("kvbo_split_decode", [_SP, _i, _i, _i, _p, _p, _i, _p, _p, _p, _p, _p, ctypes.c_float, _i, _i, _p, _p, _p, _i], _i),
     ("kvbo_fp16_storage_bound", [_SP, _p, _i, _p, _p, _p], _dbl),
     ("kvbo_i8_storage_bound", [_SP, _p, _i, _i, _p, _p, _p, _p], _dbl),
 ]:
@@ -117,6 +119,37 @@ def partition_state(shape, lens, max_len, q, k, v, part_tokens, b, h, p, scale=N
                                          _ptr(np.ascontiguousarray(v, np.float32)), sc, part_tokens, b, h, p,
                                          ctypes.byref(m), ctypes.byref(l), _ptr(o))
     return (m.value, l.value, o) if wrote else None
+
+
+KV_KIND = {np.dtype(np.float32): 0, np.dtype(np.float16): 1, np.dtype(np.int8): 2}
+
+
+def split_decode(shape, page, table, lens, max_len, q, k_pool, v_pool, k_scale=None, v_scale=None, part_tokens=0,
+                 waves=None, scale=None, threads=8):
+    """The CPU model of the split-K decode kernel over the paged pool (kvbo_split_decode):
+    (out [B][H][D], part_out [B][H][max_parts][D], part_ml [B][H][max_parts][2]). The storage type
+    comes from the pool's dtype; waves default to the kernel's (8 for int8, 4 otherwise)."""
+    kind = KV_KIND[np.dtype(k_pool.dtype)]
+    waves = (8 if kind == 2 else 4) if waves is None else waves
+    table = np.ascontiguousarray(table, np.int32)
+    lens = np.ascontiguousarray(lens, np.int32)
+    sc = scale_of(shape.head_dim) if scale is None else scale
+    part = part_tokens or auto_part_tokens(shape.batch, shape.num_kv_heads, max_len)
+    max_parts = max(1, -(-max_len // part))
+    B, H, D = shape.batch, shape.num_heads, shape.head_dim
+    out = np.full((B, H, D), np.nan, np.float32)
+    part_out = np.empty((B, H, max_parts, D), np.float32)
+    part_ml = np.empty((B, H, max_parts, 2), np.float32)
+    s = shape_of(shape)
+    k_pool, v_pool = np.ascontiguousarray(k_pool), np.ascontiguousarray(v_pool)
+    ks = None if k_scale is None else np.ascontiguousarray(k_scale, np.float32)
+    vs = None if v_scale is None else np.ascontiguousarray(v_scale, np.float32)
+    got = lib.kvbo_split_decode(ctypes.byref(s), kind, page, table.shape[1], _ptr(table), _ptr(lens), max_len,
+                                _ptr(np.ascontiguousarray(q, np.float32)), _ptr(k_pool), _ptr(v_pool), _ptr(ks),
+                                _ptr(vs), sc, part, waves, _ptr(part_out), _ptr(part_ml), _ptr(out), threads)
+    if got != max_parts:
+        raise ValueError(f"kvbo_split_decode refused its arguments ({got})")
+    return out, part_out, part_ml
 
 
 def layout_dims(lens, page, pool_factor=1.0):

@@ -1,0 +1,345 @@
+#!/usr/bin/env python3
+"""Mutation testing of this build's checks: the reference's scripts/mutation.sh, retargeted.
+
+Each mutant is one textual change to one source file. The harness copies the files a group needs
+into a scratch directory, applies the change (it must match exactly once), builds the copy on the
+CPU, runs the group's CPU tests against that build, and reports the tests that fail. A mutant is
+caught when at least one test fails; the in-tree sources and builds are never touched.
+
+Groups:
+  kernel  the reference's kernel mistakes (scripts/mutation.sh:50-59), its kernel-side boundary
+          mistakes (:33-36) and a few more, planted in the oracle's CPU model of this build's
+          split-K kernel (kvbo_split_decode in oracle/kvb_oracle.c). They are checked by
+          tests/test_split_model.py, which is the GPU parity battery (tests/parity_battery.py) run on
+          that model. No deliberately broken kernel runs on a GPU.
+  oracle  mistakes in the checker itself (fp64 attention, layout, quantiser, f16 rounding, RNG,
+          storage-error bounds), checked by tests/test_oracle.py: the pins against the reference's
+          own build, its golden vectors and closed forms.
+  host    the boundary mistakes of the C ABI and the C++ host layer (scripts/mutation.sh:37-41 and
+          their neighbours), planted in copies of kv-cache-bench_amd/ and include/, rebuilt with the
+          package Makefile (hipcc for runtime.hip), checked by tests/test_host.py, tests/test_abi.py
+          and the C++ test programs (tests/test_cpp_programs.py, CPU part).
+
+Usage:
+  python tests/mutation/mutate.py [GROUP ...] [--only SUBSTR] [--out FILE] [--keep]
+  python tests/mutation/mutate.py --check      # every mutation applies exactly once; no build
+Exit status 0 when every mutant applied, built and was caught; 1 otherwise.
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import re
+import shutil
+import signal
+import subprocess
+import sys
+import tempfile
+import time
+from dataclasses import dataclass
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+ORACLE_C = "oracle/kvb_oracle.c"
+RUNTIME = "kv-cache-bench_amd/csrc/runtime.hip"
+GROUP_TESTS = {
+    "kernel": ["tests/test_split_model.py"],
+    "oracle": ["tests/test_oracle.py"],
+    "host": ["tests/test_host.py", "tests/test_abi.py", "tests/test_cpp_programs.py"],
+}
+TEST_TIMEOUT = 900  # seconds per mutant's test run
+
+
+@dataclass(frozen=True)
+class Mutant:
+    group: str
+    name: str
+    path: str  # relative to the repository root
+    old: str
+    new: str
+
+
+def K(name, old, new):
+    return Mutant("kernel", name, ORACLE_C, old, new)
+
+
+def O(name, old, new):
+    return Mutant("oracle", name, ORACLE_C, old, new)
+
+
+def H(name, path, old, new):
+    return Mutant("host", name, path, old, new)
+
+
+MUTANTS = [
+    # ---- the kernel, in the CPU model (reference: scripts/mutation.sh:50-59, 33-36) ----
+    K("no online-softmax rescale (corr = 1)",
+      "const float corr = exp_ftz(m - m_new);", "const float corr = 1.0f;"),
+    K("accumulator rounded to fp16 each step",
+      "for (int d = 0; d < D; ++d) acc[d] += pv * vrow[i][d];",
+      "for (int d = 0; d < D; ++d) acc[d] = kvbo_f16_to_f32(kvbo_f32_to_f16(acc[d] + pv * vrow[i][d]));"),
+    K("off-by-one row inside a page",
+      "const size_t row = ((blk * Hkv + kvh) * P + t % P) * D;",
+      "const size_t row = ((blk * Hkv + kvh) * P + (t + 1) % P) * D;"),
+    K("wave merge ignores the max shift in L", "L += wl[w] * wt[w];", "L += wl[w];"),
+    K("partition merge drops the last partition",
+      "for (int i = 0; i < parts; ++i) {", "for (int i = 0; i < parts - 1; ++i) {"),
+    K("block table ignored (logical = physical)",
+      "const size_t blk = (size_t)bt[t / P];", "const size_t blk = (size_t)(t / P);"),
+    K("int8: K scale not applied", "sc[i] *= j->k_scale[blk * Hkv + kvh];", ";"),
+    K("int8: K scale of KV head 0 for every head",
+      "sc[i] *= j->k_scale[blk * Hkv + kvh];", "sc[i] *= j->k_scale[blk * Hkv];"),
+    K("int8: V dequantized with the K scale",
+      "vs[i] = j->v_scale[blk * Hkv + kvh];", "vs[i] = j->k_scale[blk * Hkv + kvh];"),
+    K("int8: V scale of the sequence's first block for every block",
+      "vs[i] = j->v_scale[blk * Hkv + kvh];", "vs[i] = j->v_scale[(size_t)bt[0] * Hkv + kvh];"),
+    K("partition merge never writes the output", "out[d] = o / L;", "(void)o;"),
+    K("partition merge takes one partition too many at an exact multiple",
+      "const int parts = (j->lens[b] + j->part_tokens - 1) / j->part_tokens;",
+      "const int parts = j->lens[b] / j->part_tokens + 1;"),
+    K("partition merge has no case for an empty sequence", "if (parts == 0) {", "if (0) {"),
+    K("query head served by the wrong KV head",
+      "const int kvh = h / (s->num_heads / Hkv);", "const int kvh = h % Hkv;"),
+    K("softmax scale not applied", "sc[i] = dot * j->scale;", "sc[i] = dot;"),
+    K("tail tile drops its last token",
+      "const int n = t1 - tt < kModelTile ? t1 - tt : kModelTile;",
+      "const int n = t1 - tt < kModelTile ? t1 - tt - 1 : kModelTile;"),
+    K("each wave skips every other tile of its stride",
+      "tt += j->waves * kModelTile", "tt += 2 * j->waves * kModelTile"),
+    K("wave merge weight exp(M - m) instead of exp(m - M)",
+      "wt[w] = exp_ftz(wm[w] - M);", "wt[w] = exp_ftz(M - wm[w]);"),
+    K("partition weight without l (w = exp(m - M))",
+      "const float w = ml[2 * i + 1] * exp_ftz(ml[2 * i] - M);", "const float w = exp_ftz(ml[2 * i] - M);"),
+    # ---- the checker ----
+    O("fp64 reference has no case for an empty sequence (scripts/mutation.sh:36)",
+      "len ? (float)(acc[d] / sum) : 0.0f", "(float)(acc[d] / sum)"),
+    O("fp64 reference: softmax scale not applied", "p[t] = dot * j->scale;", "p[t] = dot;"),
+    O("fp64 reference: max not subtracted before exp",
+      "sum += (p[t] = exp(p[t] - mx));", "sum += (p[t] = exp(p[t]));"),
+    O("fp64 reference: V read from the K cache",
+      "acc[d] += p[t] * load_elem(j->v, base + d, j->f16);", "acc[d] += p[t] * load_elem(j->k, base + d, j->f16);"),
+    O("fp64 reference: query head served by the wrong KV head",
+      "kvh = h / G, len = j->lens[b];", "kvh = h % s->num_kv_heads, len = j->lens[b];"),
+    O("max_abs_diff ignores NaN (scripts/mutation.sh:32)", "if (isnan(e)) return INFINITY;", ""),
+    O("auto_part_tokens threshold off by one (scripts/mutation.sh:41)",
+      "/ part) < 512) part /= 2;", "/ part) <= 512) part /= 2;"),
+    O("f32 -> f16 truncates", "if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) ++h;", ""),
+    O("f32 -> f16 ties away from zero", "(rest == 0x1000u && (h & 1u))", "rest == 0x1000u"),
+    O("f32 -> f16 subnormals truncate", "if (rest > half || (rest == half && (h & 1u))) ++h;", ""),
+    O("f16 -> f32 subnormal exponent off by one",
+      "bits = sign | ((uint32_t)(112 - e) << 23) | (man << 13);",
+      "bits = sign | ((uint32_t)(113 - e) << 23) | (man << 13);"),
+    O("layout: table entries past a sequence's blocks not -1",
+      "for (size_t i = 0; i < (size_t)batch * max_blocks; ++i) table[i] = -1;",
+      "for (size_t i = 0; i < (size_t)batch * max_blocks; ++i) table[i] = 0;"),
+    O("paged_index: off-by-one row inside a page",
+      "* page_size + t % page_size) * s->head_dim + d;", "* page_size + (t + 1) % page_size) * s->head_dim + d;"),
+    O("scatter reads KV head 0 for every head",
+      "src + elem_size * kvbo_contig_index(s, max_len, b, kvh, t, d)",
+      "src + elem_size * kvbo_contig_index(s, max_len, b, 0, t, d)"),
+    O("quantiser: scale from the signed maximum",
+      "const float a = fabsf(contig[kvbo_contig_index(s, max_len, b, kvh, t, d)]);",
+      "const float a = contig[kvbo_contig_index(s, max_len, b, kvh, t, d)];"),
+    O("quantiser truncates instead of rounding to nearest even",
+      "float r = nearbyintf(x / scale);", "float r = truncf(x / scale);"),
+    O("quantiser: scale max / 128", "const float scale = amax / 127.0f;", "const float scale = amax / 128.0f;"),
+    O("dequantiser: scale of KV head 0 for every head",
+      "t / page_size] * s->num_kv_heads + kvh];", "t / page_size] * s->num_kv_heads];"),
+    O("mt19937_64: wrong tempering shift", "x ^= x >> 43;", "x ^= x >> 42;"),
+    O("partition state drops the last token of a full partition",
+      "const int t1 = len < t0 + part_tokens ? len : t0 + part_tokens;",
+      "const int t1 = len < t0 + part_tokens ? len : t0 + part_tokens - 1;"),
+    O("fp16 storage bound without the V rounding term",
+      "return vmax * (u + expm1(2 * E)) + 2e-5;", "return vmax * expm1(2 * E) + 2e-5;"),
+    O("fp16 storage bound without the score term",
+      "return vmax * (u + expm1(2 * E)) + 2e-5;", "return vmax * u + 2e-5;"),
+    O("int8 storage bound without the V rounding term",
+      "return vmax * expm1(2 * E) + vq + 2e-5;", "return vmax * expm1(2 * E) + 2e-5;"),
+    O("int8 storage bound without the score term",
+      "return vmax * expm1(2 * E) + vq + 2e-5;", "return vq + 2e-5;"),
+    # ---- the C ABI and the host layer (scripts/mutation.sh:37-41) ----
+    H("capacity + 1 accepted", RUNTIME, "(size_t)len > capacity)", "(size_t)len > capacity + 1)"),
+    H("exactly the capacity refused", RUNTIME, "(size_t)len > capacity)", "(size_t)len >= capacity)"),
+    H("length past max_len accepted", RUNTIME, "len < 0 || len > max_len || (size_t)len", "len < 0 || (size_t)len"),
+    H("length check skips the last sequence", RUNTIME,
+      "for (int b = 0; b < batch; ++b) {\n        const int len = lens[b];",
+      "for (int b = 0; b < batch - 1; ++b) {\n        const int len = lens[b];"),
+    H("auto_part_tokens threshold off by one (C ABI)", RUNTIME,
+      "/ part) < 512) part /= 2;", "/ part) <= 512) part /= 2;"),
+    H("auto_part_tokens threshold off by one (C++ header)", "include/kvb/hip_attn.hpp",
+      "/ part) < 512) part /= 2;", "/ part) <= 512) part /= 2;"),
+    H("max_abs_diff ignores NaN (C++ header)", "include/kvb/layout.hpp", "if (std::isnan(e)) return INFINITY;", ""),
+    H("more than 65535 partitions accepted", RUNTIME, "if (max_parts_of(a) > 65535)", "if (false)"),
+    H("int8 cache without scales accepted", RUNTIME,
+      "if (a->kv_type == KVB_KV_I8 && (!a->k_scale || !a->v_scale))", "if (false)"),
+    H("undersized caller workspace accepted", RUNTIME,
+      "if (a->workspace && a->workspace_bytes < workspace_need(a))", "if (false)"),
+    H("workspace size without the (m, l) slots", RUNTIME, " + slots * sizeof(float2);", ";"),
+    H("head count not a multiple of the KV heads accepted", RUNTIME, "if (H % Hkv != 0)", "if (false)"),
+    H("writer: int8 without scales accepted", RUNTIME, "|| (a->kv_type == KVB_KV_I8 && !a->scales)", ""),
+    H("host quantiser truncates", "kv-cache-bench_amd/host/layout.cpp",
+      "std::nearbyint(row[d] / scale)", "std::trunc(row[d] / scale)"),
+    H("host layout: table entries past a sequence's blocks not -1", "kv-cache-bench_amd/host/layout.cpp",
+      "L.block_table.assign(seq_lens.size() * size_t(L.max_blocks), -1);",
+      "L.block_table.assign(seq_lens.size() * size_t(L.max_blocks), 0);"),
+    H("host paged_index: off-by-one row inside a page", "include/kvb/layout.hpp",
+      "t % L.page_size) * s.head_dim + d;", "(t + 1) % L.page_size) * s.head_dim + d;"),
+]
+
+
+class NotApplied(Exception):
+    pass
+
+
+def mutated_text(m: Mutant, text: str) -> str:
+    n = text.count(m.old)
+    if n != 1:
+        raise NotApplied(f"{m.path}: the text to replace occurs {n} times")
+    return text.replace(m.old, m.new)
+
+
+def check_all(mutants=MUTANTS) -> list[str]:
+    """Problems with the mutant list against the current sources (empty when every mutant applies)."""
+    problems, seen = [], set()
+    for m in mutants:
+        if m.name in seen:
+            problems.append(f"duplicate name: {m.name}")
+        seen.add(m.name)
+        if m.group not in GROUP_TESTS:
+            problems.append(f"{m.name}: unknown group {m.group}")
+        try:
+            with open(os.path.join(ROOT, m.path)) as f:
+                mutated_text(m, f.read())
+        except (OSError, NotApplied) as e:
+            problems.append(f"{m.name}: {e}")
+    return problems
+
+
+def _copy(rel, dst_root, ignore=None):
+    src = os.path.join(ROOT, rel)
+    dst = os.path.join(dst_root, rel)
+    os.makedirs(os.path.dirname(dst), exist_ok=True)
+    if os.path.isdir(src):
+        shutil.copytree(src, dst, symlinks=True, ignore=ignore)  # copy2: modification times kept
+    else:
+        shutil.copy2(src, dst)
+
+
+def prepare(m: Mutant, work: str) -> tuple[dict, str]:
+    """Copies what the mutant's group builds, applies the mutant and builds. Returns the
+    environment for the test run and the build log."""
+    env = dict(os.environ)
+    if m.group in ("kernel", "oracle"):
+        for f in ("oracle/Makefile", "oracle/kvb_oracle.h", ORACLE_C):
+            _copy(f, work)
+        cmd = ["make", "-C", os.path.join(work, "oracle"), "all"]
+        env["KVBO_LIB"] = os.path.join(work, "oracle", "build", "libkvb_oracle.so")
+    else:
+        skip = shutil.ignore_patterns("__pycache__")
+        for d in ("kv-cache-bench_amd", "include", "tests/cpp"):
+            _copy(d, work, skip)
+        for f in ("oracle/kvb_oracle.h", "oracle/build/libkvb_oracle.so"):
+            _copy(f, work)
+        cmd = ["make", "-C", os.path.join(work, "kv-cache-bench_amd"), "-j8"]
+        env["KVB_BUILD_DIR"] = os.path.join(work, "kv-cache-bench_amd", "build")
+    path = os.path.join(work, m.path)
+    with open(path) as f:
+        text = mutated_text(m, f.read())
+    with open(path, "w") as f:
+        f.write(text)
+    later = time.time() + 2  # newer than every copied object, so make rebuilds what depends on it
+    os.utime(path, (later, later))
+    b = subprocess.run(cmd, capture_output=True, text=True)
+    if b.returncode:
+        raise RuntimeError("does not build:\n" + (b.stdout + b.stderr)[-2000:])
+    return env, b.stdout
+
+
+def run_tests(m: Mutant, env: dict, fail_fast=False):
+    """(caught, summary). Runs the group's tests in a child process group of its own."""
+    cmd = [sys.executable, "-m", "pytest", *GROUP_TESTS[m.group], "-q", "-m", "not gpu", "-rf",
+           "-p", "no:cacheprovider", "-o", "console_output_style=classic"]
+    if fail_fast:
+        cmd.append("-x")
+    p = subprocess.Popen(cmd, cwd=ROOT, env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                         start_new_session=True)
+    try:
+        out, _ = p.communicate(timeout=TEST_TIMEOUT)
+    except subprocess.TimeoutExpired:
+        os.killpg(p.pid, signal.SIGKILL)  # the process group started above, nothing else
+        p.communicate()
+        return True, f"tests timed out after {TEST_TIMEOUT} s"
+    if p.returncode < 0:
+        return True, f"test process died with signal {-p.returncode}"
+    lines = out.strip().splitlines()
+    tail = lines[-1] if lines else ""
+    failed = [ln.split(" ", 1)[1].split(" - ", 1)[0] for ln in lines if ln.startswith("FAILED ")]
+    failed = [f.replace("tests/", "", 1) for f in failed]
+    counts = re.findall(r"(\d+) (passed|failed|error)", tail)
+    summary = ", ".join(f"{n} {w}" for n, w in counts) or tail
+    if p.returncode == 1:
+        shown = "; ".join(failed[:3]) + (f"; +{len(failed) - 3} more" if len(failed) > 3 else "")
+        return True, f"{summary}: {shown}"
+    if p.returncode == 0:
+        return False, f"{summary}"
+    return False, f"pytest exit {p.returncode}: {tail}"
+
+
+def run_one(m: Mutant, keep=False, fail_fast=False):
+    work = tempfile.mkdtemp(prefix="kvb-mutant-")
+    try:
+        try:
+            env, _ = prepare(m, work)
+        except (NotApplied, RuntimeError) as e:
+            return "error", str(e)
+        caught, summary = run_tests(m, env, fail_fast)
+        return ("caught" if caught else "NOT CAUGHT"), summary
+    finally:
+        if not keep:
+            shutil.rmtree(work, ignore_errors=True)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("groups", nargs="*", metavar="GROUP", help=f"any of {', '.join(GROUP_TESTS)} (default: all)")
+    ap.add_argument("--only", help="run the mutants whose name contains this text")
+    ap.add_argument("--check", action="store_true", help="only check that every mutation applies")
+    ap.add_argument("--out", help="also write the report to this file")
+    ap.add_argument("--keep", action="store_true", help="keep the scratch directories")
+    a = ap.parse_args(argv)
+    unknown = [g for g in a.groups if g not in GROUP_TESTS]
+    if unknown:
+        ap.error(f"unknown group(s) {unknown}; choose from {list(GROUP_TESTS)}")
+    problems = check_all()
+    if a.check:
+        for p in problems:
+            print(p)
+        print(f"{len(MUTANTS)} mutants, {len(problems)} problems")
+        return 1 if problems else 0
+    groups = a.groups or list(GROUP_TESTS)
+    todo = [m for m in MUTANTS if m.group in groups and (not a.only or a.only in m.name)]
+    report, bad = [], 0
+    for g in groups:
+        ms = [m for m in todo if m.group == g]
+        if not ms:
+            continue
+        head = f"== {g}: {len(ms)} mutants, tests: {' '.join(GROUP_TESTS[g])}"
+        print(head, flush=True)
+        report.append(head)
+        for m in ms:
+            t0 = time.time()
+            status, summary = run_one(m, a.keep)
+            line = f"{m.name}: {status} ({summary}) [{time.time() - t0:.0f} s]"
+            print(line, flush=True)
+            report.append(line)
+            bad += status != "caught"
+    tail = f"{len(todo)} mutants, {len(todo) - bad} caught, {bad} not caught or not built"
+    print(tail)
+    report.append(tail)
+    if a.out:
+        with open(a.out, "w") as f:
+            f.write("\n".join(report) + "\n")
+    return 1 if bad else 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

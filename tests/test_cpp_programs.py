@@ -7,7 +7,9 @@ import pytest
 
 from conftest import ROOT, progress
 
-BIN = os.path.join(ROOT, "kv-cache-bench_amd", "build", "tests")
+# KVB_BUILD_DIR: programs built from a mutated copy of the sources (tests/mutation/mutate.py)
+BUILD = os.environ.get("KVB_BUILD_DIR") or os.path.join(ROOT, "kv-cache-bench_amd", "build")
+BIN = os.path.join(BUILD, "tests")
 
 
 def run(name, timeout):
@@ -55,7 +57,7 @@ def test_boundary_tests(gpu):
     assert rc == 0, out[-4000:]
 
 
-KVBENCH = os.path.join(ROOT, "kv-cache-bench_amd", "build", "kvbench")
+KVBENCH = os.path.join(BUILD, "kvbench")
 
 
 @pytest.mark.gpu

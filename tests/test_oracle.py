@@ -188,6 +188,71 @@ def test_quantizer_closed_form(oracle):
     assert big > 6 * small > 0 and zero == 0
 
 
+def test_fp16_storage_bound_sound_where_each_term_is_needed(oracle):
+    """The fp16 storage-error bound (tests/gpu_tests.cpp:19-40) holds on two constructed cases,
+    each of which exceeds what the bound would be without one of its terms."""
+    u = 2.0 ** -11
+    # (a) q = 0 (no score error) and every V element the tie 1 + 2^-11, which rounds down to 1:
+    # the output moves by exactly u, more than the fp32 tolerance alone.
+    s = S(1, 2, 1, 64)
+    q = np.zeros((1, 2, 64), np.float32)
+    k32 = rand((1, 1, 5, 64), 21)
+    v32 = np.full((1, 1, 5, 64), 1 + u, np.float32)
+    exact = oracle.attention(s, [5], 5, q, k32, v32)
+    stored = oracle.attention(s, [5], 5, q, k32.astype(np.float16), v32.astype(np.float16))
+    err = oracle.max_abs_diff(stored, exact)
+    assert err == u
+    assert err <= oracle.fp16_storage_bound(s, [5], 5, q, k32, v32)
+    # (b) two K rows that round to the same fp16 row from either side (1 + 2^-11 down, 1 - 2^-12 up,
+    # a tie to even) under a large query: the stored scores tie, the exact ones differ by
+    # x (2^-11 + 2^-12) with x = scale * sum q = 1000, and with V = +1 / -1 the output moves by
+    # tanh(x * 3 * 2^-13), about 0.35: far beyond u max|v|.
+    s = S(1, 1, 1, 128)
+    q = np.full((1, 1, 128), 1000 / np.sqrt(128), np.float32)
+    k32 = np.stack([np.full(128, 1 + u), np.full(128, 1 - u / 2)]).astype(np.float32).reshape(1, 1, 2, 128)
+    v32 = np.stack([np.ones(128), -np.ones(128)]).astype(np.float32).reshape(1, 1, 2, 128)
+    assert np.array_equal(k32[0, 0, 0].astype(np.float16), k32[0, 0, 1].astype(np.float16))
+    exact = oracle.attention(s, [2], 2, q, k32, v32)
+    stored = oracle.attention(s, [2], 2, q, k32.astype(np.float16), v32.astype(np.float16))
+    err = oracle.max_abs_diff(stored, exact)
+    assert abs(err - np.tanh(1000 * 3 * 2.0 ** -13)) < 1e-3 and not stored.any()
+    assert err <= oracle.fp16_storage_bound(s, [2], 2, q, k32, v32)
+
+
+def test_i8_storage_bound_sound_where_each_term_is_needed(oracle):
+    """The int8 storage-error bound (tests/gpu_tests.cpp:42-62) likewise: two tokens in one page,
+    so one scale per K and per V."""
+    s = S(1, 1, 1, 64)
+    table = oracle.make_paged_layout([2], 2, 5)
+
+    def err_and_bound(q, k32, v32):
+        kq, ks = oracle.quantize(s, 2, table, [2], 2, k32, 1)
+        vq, vs = oracle.quantize(s, 2, table, [2], 2, v32, 1)
+        kd = oracle.dequantize(s, 2, table, [2], 2, kq, ks)
+        vd = oracle.dequantize(s, 2, table, [2], 2, vq, vs)
+        err = oracle.max_abs_diff(oracle.attention(s, [2], 2, q, kd, vd), oracle.attention(s, [2], 2, q, k32, v32))
+        return err, oracle.i8_storage_bound(s, [2], 2, table, q, ks, vs)
+
+    # (a) q = 0: one token's V row sets the scale 1/127, the other's 0.49/127 all round to 0; the
+    # mean moves by 0.49/127/2, about the V term s_v / 2 = 1/254 and far beyond the fp32 tolerance.
+    q = np.zeros((1, 1, 64), np.float32)
+    k32 = rand((1, 1, 2, 64), 22)
+    v32 = np.stack([np.ones(64), np.full(64, 0.49 / 127)]).astype(np.float32).reshape(1, 1, 2, 64)
+    err, bound = err_and_bound(q, k32, v32)
+    assert abs(err - 0.49 / 127 / 2) < 1e-6 and err <= bound
+    # (b) K rows [1, 0.49/127 ...] and [1, 0 ...] quantise to the same row, so the stored scores tie;
+    # with q = 30 on dims 1..63 the exact scores differ by 30 * 63 * 0.49 / 127 / 8, about 0.91, and
+    # with V = +1 / -1 the output moves by tanh(0.455): far beyond the V term.
+    q = np.zeros((1, 1, 64), np.float32)
+    q[0, 0, 1:] = 30
+    k32 = np.zeros((1, 1, 2, 64), np.float32)
+    k32[0, 0, :, 0] = 1
+    k32[0, 0, 0, 1:] = 0.49 / 127
+    v32 = np.stack([np.ones(64), -np.ones(64)]).astype(np.float32).reshape(1, 1, 2, 64)
+    err, bound = err_and_bound(q, k32, v32)
+    assert abs(err - np.tanh(30 * 63 * 0.49 / 127 / 8 / 2)) < 1e-3 and err <= bound
+
+
 @pytest.mark.skipif(not os.path.exists(os.path.join(ROOT, "oracle", "_ref", "libkvbref.so")), reason="oracle/_ref not built")
 class TestAgainstReferenceBuild:
     """The reference's own src/reference.cpp, compiled into oracle/_ref, on the same inputs."""
