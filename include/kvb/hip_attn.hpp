@@ -73,8 +73,7 @@ inline int auto_part_tokens(const Shape& s, int max_len) {
 // per token; enough workgroups keep enough bytes in flight. Measured on MI355X (c4): fastest at
 // one workgroup per CU (min_groups 256, the default).
 int mi355x_part_tokens(const Shape& s, int max_len, int min_groups = 256, int min_part = 256, int max_part = 4096);
-// min_groups of the policy for a storage type: 256 (one workgroup per CU) for every type; an int8
-// workgroup has twice the waves of an fp16 one, so both keep the same waves per SIMD.
+// min_groups of the policy for a storage type: 256 (one workgroup per CU) for every type.
 inline int mi355x_min_groups(KvType) { return 256; }
 
 struct PagedArgs {

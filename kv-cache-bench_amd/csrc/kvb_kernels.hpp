@@ -11,12 +11,11 @@ namespace kvbk {
 
 enum KvKind { KV_F32 = 0, KV_F16 = 1, KV_I8 = 2 };
 
-// Waves per paged_decode workgroup (the reference's kSimdGroups, 4 for every type,
-// src/metal_attn.hpp:41). int8 tiles carry half the bytes of fp16 ones, so an int8 workgroup has 8
-// waves: the same waves per SIMD from half as many partitions, which halves the partial results to
-// merge. Measured on c4-shaped int8: 52 us at 8 waves x 4096-token partitions against 53 us at
-// 4 x 2048; fp16 is best at 4.
-constexpr int decode_waves(int kind) { return kind == KV_I8 ? 8 : 4; }
+// Waves per paged_decode workgroup: 4 for every type, as the reference's kSimdGroups
+// (src/metal_attn.hpp:41), one per SIMD. With 8 int8 waves (two per SIMD) the second wave on each
+// SIMD ended its loop about 7 us after the first on c4, and the workgroup waited for it: measured on
+// MI355X, int8 at 4 waves takes 47.2 us on c4 (8 waves: 48.8), 211 us on c5 (223), and c3 the same.
+constexpr int decode_waves(int /*kind*/) { return 4; }
 // Tokens one wave handles per step of its loop: the N of a 16x16 MFMA tile.
 constexpr int kTile = 16;
 

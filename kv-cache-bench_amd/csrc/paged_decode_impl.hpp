@@ -180,8 +180,8 @@ __device__ __forceinline__ float load_agent(float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// (waves_per_eu(2): two waves per SIMD, 8 per CU, keep two tiles per wave in flight; the register
-// budget that leaves is 256 per lane)
+// (waves_per_eu(2): up to two waves per SIMD, two workgroups per CU, each wave keeping one tile in
+// flight while it computes another; the register budget that leaves is 256 per lane)
 template <int KIND, int D, int QG, bool FAST>
 __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(DecodeParams p) {
     using T = KvT<KIND, D>;

@@ -128,9 +128,9 @@ def split_decode(shape, page, table, lens, max_len, q, k_pool, v_pool, k_scale=N
                  waves=None, scale=None, threads=8):
     """The CPU model of the split-K decode kernel over the paged pool (kvbo_split_decode):
     (out [B][H][D], part_out [B][H][max_parts][D], part_ml [B][H][max_parts][2]). The storage type
-    comes from the pool's dtype; waves default to the kernel's (8 for int8, 4 otherwise)."""
+    comes from the pool's dtype; waves default to the kernel's 4 per workgroup."""
     kind = KV_KIND[np.dtype(k_pool.dtype)]
-    waves = (8 if kind == 2 else 4) if waves is None else waves
+    waves = 4 if waves is None else waves
     table = np.ascontiguousarray(table, np.int32)
     lens = np.ascontiguousarray(lens, np.int32)
     sc = scale_of(shape.head_dim) if scale is None else scale

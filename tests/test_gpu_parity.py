@@ -170,10 +170,11 @@ def test_fused_merge_reads_fresh_partitions(gpu):
 
 @pytest.mark.parametrize("kv,part", pb.MANY_PARTITIONS)
 def test_many_partitions(gpu, oracle, kv, part):
-    """Partition counts at and past what the fused merge stages in LDS: at head_dim 64 and 8 heads
-    per group, f16 part 64 (64 partitions) and i8 part 32 (128) fill it exactly; the others exceed
-    it and the runtime merges with paged_reduce as a second kernel. The fused output equals the
-    two-kernel output bit for bit."""
+    """Partition counts below, at and past what the fused merge stages in LDS (1024 (m, l) pairs
+    for f16 and i8 at head_dim 64, 4096 for f32): with 8 heads per group, f16 part 64 (64
+    partitions) is below it, f16 and i8 part 32 (128) fill it exactly, f16 and i8 part 16 (256)
+    exceed it and the runtime merges with paged_reduce as a second kernel. The fused output equals
+    the two-kernel output bit for bit."""
     kvb = gpu
     got = pb.check_many_partitions(kvb, oracle, runner(kvb), kv, part)
     w, c = pb.many_partitions_case(kvb, kv)
