@@ -43,7 +43,16 @@ struct DecodeParams {
     // qg * max_parts <= fused_merge_slots(kind, head_dim).
     float* out;                 // [B][H][D]
     int* counters;              // [B][H / qg]
+    int batch;
+    // Nonzero: a ragged batch in longest-first order. Grid y enumerates this many work items (see
+    // ragged_item in paged_decode_impl.hpp) instead of grid (y, z) = (sequence, partition).
+    // Requires batch <= kRaggedMaxBatch and part_tokens < 65536.
+    int ragged_items;
 };
+
+// Ragged batches up to this many sequences use the longest-first work order (one lane per
+// sequence, 8 sequences per lane at most).
+constexpr int kRaggedMaxBatch = 512;
 
 // Weight of one partition in the merge, w = l exp(m - M) (m, M in natural-log units). paged_reduce
 // and the fused merge both use it, then sum L += w and o = fma(w, o_i, o) in partition order, so
@@ -101,8 +110,8 @@ inline void launch_marked(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipSt
         hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
 }
 
-// paged_decode for one storage kind: grid (H / qg, batch, max_parts), decode_waves(kind) waves per
-// workgroup. `fast`: every 16-token tile lies inside one page (page_size % 16 == 0 and
+// paged_decode for one storage kind: grid (H / qg, batch, max_parts), or (H / qg, ragged_items, 1)
+// for a ragged batch, decode_waves(kind) waves per workgroup. `fast`: every 16-token tile lies inside one page (page_size % 16 == 0 and
 // part_tokens % 16 == 0), so block ids and scales are read once per tile.
 hipError_t launch_paged_decode_f32(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s,
                                    const Marks& m = {});

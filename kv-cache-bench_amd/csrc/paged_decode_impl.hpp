@@ -180,6 +180,95 @@ __device__ __forceinline__ float load_agent(float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---- longest-first work order for ragged batches ---------------------------------------------
+// With DecodeParams::ragged_items set, grid y enumerates work items rather than (sequence,
+// partition) pairs: first every full partition (len / part_tokens per sequence, in sequence order),
+// then each sequence's partial last partition, longest first (ties: lower sequence first), then one
+// item per empty sequence (whose output is written as 0). The longest pieces start first and the
+// short ones fill the end; in the plain order the partial last partitions of the longest sequences
+// started last, and the step ended on them (c5: 363 -> 341 us fp16, 203 -> 183 us int8 on MI355X).
+// A partition is computed by the same code whatever its position, so the results are the same bits.
+// Each wave finds its workgroup's item from seq_lens, one lane per sequence.
+struct WorkItem {
+    int b, part;  // b < 0: no such item (the host's lengths and seq_lens disagree)
+};
+
+// Inclusive prefix sum over the 64 lanes with DPP: row shifts 1, 2, 4, 8 within each 16-lane row,
+// then row 0's total into row 1 and row 2's into row 3 (row_bcast:15), then rows 0-1's into rows
+// 2-3 (row_bcast:31). Lanes a shift or a row mask leaves out read the `old` operand, 0.
+__device__ __forceinline__ int wave_inclusive_sum(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15, rows 1 and 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31, rows 2 and 3
+    return x;
+}
+
+__device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int batch, int part_tokens, int i) {
+    constexpr int E = kRaggedMaxBatch / 64;
+    const int lane = threadIdx.x & 63;
+    const int ne = (batch + 63) >> 6;
+    int len[E];
+    for (int e = 0; e < E; ++e) len[e] = (e < ne && 64 * e + lane < batch) ? seq_lens[64 * e + lane] : 0;
+    WorkItem r{-1, 0};
+    // full partitions, in sequence order: an exclusive scan of len / part_tokens
+    int before = 0;
+    for (int e = 0; e < E && e < ne; ++e) {
+        const int f = len[e] / part_tokens;
+        const int s = wave_inclusive_sum(f);
+        const int excl = before + s - f;
+        const unsigned long long hit = __ballot(f > 0 && excl <= i && i < excl + f);
+        if (hit) {
+            const int l = __ffsll(hit) - 1;
+            r = WorkItem{64 * e + l, i - __builtin_amdgcn_readlane(excl, l)};
+        }
+        before += __builtin_amdgcn_readlane(s, 63);
+    }
+    if (r.b < 0) {
+        // partial last partitions, longest first: the (i - full)-th largest key rem << 16 | (0xFFFF - b),
+        // found bit by bit from the top (keys are distinct; 0 marks a sequence without one)
+        int j = i - before, npart = 0;
+        unsigned key[E];
+        for (int e = 0; e < E; ++e) {
+            const int rem = len[e] % part_tokens;
+            key[e] = (e < ne && rem > 0) ? ((unsigned)rem << 16) | (0xFFFFu - (unsigned)(64 * e + lane)) : 0u;
+            if (e < ne) npart += __popcll(__ballot(key[e] != 0u));
+        }
+        if (j < npart) {
+            unsigned want = 0;
+            const int top = 16 + (32 - __builtin_clz((unsigned)part_tokens));  // keys < 2^top
+            for (int bit = min(top, 32) - 1; bit >= 0; --bit) {
+                const unsigned cand = want | (1u << bit), hi = ~0u << bit;
+                int cnt = 0;
+                for (int e = 0; e < E && e < ne; ++e) cnt += __popcll(__ballot((key[e] & hi) == cand));
+                if (j < cnt) want = cand;
+                else j -= cnt;
+            }
+            const int b = 0xFFFF - (int)(want & 0xFFFFu);
+            int lb = 0;
+            for (int e = 0; e < E && e < ne; ++e)
+                if (e == (b >> 6)) lb = __builtin_amdgcn_readlane(len[e], b & 63);
+            r = WorkItem{b, lb / part_tokens};
+        } else {
+            // empty sequences, in sequence order
+            int k = j - npart;
+            for (int e = 0; e < E && e < ne; ++e) {
+                const unsigned long long m = __ballot(len[e] == 0 && 64 * e + lane < batch);
+                const int c = __popcll(m);
+                if (r.b < 0 && k < c) {
+                    const int rank = __popcll(m & ((1ull << lane) - 1ull));
+                    const unsigned long long hit = __ballot(((m >> lane) & 1ull) && rank == k);
+                    r = WorkItem{64 * e + __ffsll(hit) - 1, 0};
+                }
+                k -= c;
+            }
+        }
+    }
+    return WorkItem{__builtin_amdgcn_readfirstlane(r.b), __builtin_amdgcn_readfirstlane(r.part)};
+}
+
 // (waves_per_eu(2): up to two waves per SIMD, two workgroups per CU, each wave keeping one tile in
 // flight while it computes another; the register budget that leaves is 256 per lane)
 template <int KIND, int D, int QG, bool FAST>
@@ -206,7 +295,13 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // every partition's work over all XCDs. With the partition fastest, the XCD followed the
     // partition index, and the partitions that short sequences leave empty left XCDs idle (c5
     // fp16: 486 -> 366 us; equal lengths under a longer max_len ran 1.7x slower).
-    const int part = blockIdx.z, b = blockIdx.y;
+    int part = blockIdx.z, b = blockIdx.y;
+    if (p.ragged_items) {
+        const WorkItem it = ragged_item(p.seq_lens, p.batch, p.part_tokens, blockIdx.y);
+        if (it.b < 0 || it.b >= p.batch || it.part >= p.max_parts) return;  // uniform, before any barrier
+        b = it.b;
+        part = it.part;
+    }
     const int h0 = blockIdx.x * QG;
     const int len = p.seq_lens[b];
     const int t0 = part * p.part_tokens;
@@ -626,7 +721,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
 
 template <int KIND, int D, int QG, bool FAST>
 hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
-    const dim3 grid(p.num_heads / QG, batch, p.max_parts);
+    const dim3 grid(p.num_heads / QG, p.ragged_items ? p.ragged_items : batch, p.ragged_items ? 1 : p.max_parts);
     launch_marked(paged_decode_kernel<KIND, D, QG, FAST>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
     return hipGetLastError();
 }

@@ -180,6 +180,21 @@ struct StepMarks {
     kvbk::Marks step, decode, reduce;
 };
 
+// Work items of a ragged batch in the kernel's longest-first order (one per partition holding
+// tokens, one per empty sequence), or 0 for the plain (sequence, partition) grid: sequences of equal
+// length gain nothing from reordering, and the order needs one lane per sequence.
+int ragged_items(const kvb_paged_args* a, int part) {
+    if (a->batch < 2 || a->batch > kvbk::kRaggedMaxBatch || part >= 65536) return 0;
+    const int32_t* lens = a->host_seq_lens;
+    bool equal = true;
+    long long items = 0;
+    for (int b = 0; b < a->batch; ++b) {
+        equal = equal && lens[b] == lens[0];
+        items += std::max(1LL, ((long long)lens[b] + part - 1) / part);
+    }
+    return equal || items > 65535 ? 0 : (int)items;
+}
+
 int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, bool fused, const StepMarks& mk) {
     const int part = resolve_part(a);
     const int qg = query_heads_per_group(a);
@@ -201,6 +216,8 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     p.max_parts = max_parts_of(a);
     p.part_tokens = part;
     p.qscale = (1.0f / std::sqrt((float)a->head_dim)) * 1.4426950408889634f;
+    p.batch = a->batch;
+    p.ragged_items = ragged_items(a, part);
     // fused merge when the group's partition (m, l) pairs fit its LDS staging
     if (fused && qg * p.max_parts > kvbk::fused_merge_slots(a->kv_type, a->head_dim)) fused = false;
     if (fused) {

@@ -90,6 +90,36 @@ def test_huge_and_tiny_queries(gpu, oracle):
     pb.check_huge_and_tiny_queries(gpu, oracle, runner(gpu))
 
 
+@pytest.mark.parametrize("kv", ["f32", "f16", "i8"])
+def test_ragged_batch_equals_each_sequence_alone(gpu, kv):
+    """A ragged batch runs in the longest-first work order (grid y enumerates partitions, the
+    largest first); a batch of one runs in the plain (sequence, partition) grid. Every partition is
+    computed by the same code either way, so each sequence's output in the batch must equal its
+    output run alone bit for bit, fused and two-kernel: a partition computed twice, skipped, or
+    given to the wrong sequence cannot pass."""
+    kvb = gpu
+    lens = [0, 1, 255, 256, 257, 1000, 4096, 5000, 63, 0, 2049, 700]
+    part = 256
+    w = kvb.Workload(kvb.Shape(len(lens), 8, 2, 128), kv, lens, seed=101, varied=(kv == "i8"))
+    c = kvb.PagedCache(w, 16, 5, pool_factor=1.5, poison=True)
+    dev = kvb.DeviceCase(w, c)
+    dev.out.fill(0xFF)
+    dev.run(part)
+    fused = dev.output()
+    dev.out.fill(0xFF)
+    dev.run_split(part)
+    assert np.array_equal(fused, dev.output())
+    dev.free()
+    for b, L in enumerate(lens):
+        n = max(L, 1)
+        one = kvb.Workload.from_arrays(kv, [L], w.q[b:b + 1], w.k[b:b + 1, :, :n], w.v[b:b + 1, :, :n])
+        d1 = kvb.DeviceCase(one, kvb.PagedCache(one, 16, 7 + b, pool_factor=1.5, poison=True))
+        d1.out.fill(0xFF)
+        d1.run(part)
+        assert np.array_equal(d1.output()[0], fused[b]), (b, L)
+        d1.free()
+
+
 def test_naive_matches_oracle(gpu, oracle):
     kvb = gpu
     for kv in ("f32", "f16"):
