@@ -71,7 +71,7 @@ typedef struct kvb_paged_args {
     const int32_t* block_table;  /* device, int32 [B][max_blocks]; logical block i of sequence b
                                     lives in physical block block_table[b*max_blocks + i] */
     const int32_t* seq_lens;     /* device, int32 [B] */
-    const int32_t* host_seq_lens;/* host copy of seq_lens, read by the capacity check */
+    const int32_t* host_seq_lens;/* host copy of seq_lens, equal to it: capacity check, launch size */
     float* out;                  /* device, float [B][H][D] */
     const float* k_scale;        /* device, float [blocks][Hkv]; required for I8 */
     const float* v_scale;
