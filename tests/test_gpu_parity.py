@@ -120,6 +120,27 @@ def test_ragged_batch_equals_each_sequence_alone(gpu, kv):
         d1.free()
 
 
+@pytest.mark.parametrize("batch", [2, 65, 300, 512, 513])
+def test_ragged_order_at_every_batch_width(gpu, oracle, batch):
+    """The longest-first order keeps one lane per sequence and up to 8 sequences per lane (512);
+    513 sequences fall back to the plain grid. Random lengths with empty and exact-multiple ones,
+    against the oracle; empty sequences exactly 0."""
+    kvb = gpu
+    g = np.random.Generator(np.random.PCG64(batch))
+    lens = g.integers(0, 400, size=batch)
+    lens[::7] = 0
+    lens[1::11] = 128
+    lens[0] = 399
+    w = kvb.Workload(kvb.Shape(batch, 4, 2, 64), "f16", lens.tolist(), seed=batch)
+    c = kvb.PagedCache(w, 16, batch, pool_factor=1.25, poison=True)
+    want, tol = pb.expected(kvb, oracle, w, c)
+    for part in (64, 1000):
+        got = run(kvb, w, c, part)
+        assert oracle.max_abs_diff(got, want) <= tol, part
+        for b in np.flatnonzero(w.lens == 0):
+            assert not got[b].any(), (part, b)
+
+
 def test_naive_matches_oracle(gpu, oracle):
     kvb = gpu
     for kv in ("f32", "f16"):
