@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <memory>
+#include <span>
 #include <string>
 #include <vector>
 
@@ -73,6 +74,13 @@ inline int auto_part_tokens(const Shape& s, int max_len) {
 // per token; enough workgroups keep enough bytes in flight. Measured on MI355X (c4): fastest at
 // one workgroup per CU (min_groups 256, the default).
 int mi355x_part_tokens(const Shape& s, int max_len, int min_groups = 256, int min_part = 256, int max_part = 4096);
+// The policy for a batch given its lengths. Lengths that are not all equal make a ragged batch,
+// which runs in the longest-first work order. There, shorter partitions give the schedule finer
+// pieces at its end, so max_part is capped at kRaggedMaxPart. Measured on MI355X (c5): 330 us at
+// 2048 against 340 us at 4096 (fp16), 182 against 183 (int8).
+constexpr int kRaggedMaxPart = 2048;
+int mi355x_part_tokens(const Shape& s, std::span<const int> lens, int min_groups = 256, int min_part = 256,
+                       int max_part = 4096);
 // min_groups of the policy for a storage type: 256 (one workgroup per CU) for every type.
 inline int mi355x_min_groups(KvType) { return 256; }
 

@@ -113,6 +113,7 @@ _HOST_SIGS = {
     "kvbh_dequantize_paged_i8": ([_i, _i, _i, _i, _i, _p, _p, _i, _p, _p, _p], _i),
     "kvbh_poison_paged": ([_i, _i, _i, _i, _i, _i, _p, _p, _sz, _p, _p], _i),
     "kvbh_mi355x_part_tokens": ([_i, _i, _i, _i, _i, _i, _i, _i], _i),
+    "kvbh_mi355x_part_tokens_lens": ([_i, _i, _i, _i, _p, _i, _i, _i], _i),
 }
 for _name, (_args, _ret) in _HOST_SIGS.items():
     _f = getattr(host, _name)
@@ -165,6 +166,14 @@ def mi355x_part_tokens(shape, max_len, min_groups=256, min_part=256, max_part=40
     """The MI355X partition policy (kvb::mi355x_part_tokens, include/kvb/hip_attn.hpp)."""
     return host.kvbh_mi355x_part_tokens(shape.batch, shape.num_heads, shape.num_kv_heads, shape.head_dim, max_len,
                                         min_groups, min_part, max_part)
+
+
+def mi355x_part_tokens_for(shape, lens, min_groups=256, min_part=256, max_part=4096) -> int:
+    """The MI355X partition policy given the batch's lengths (kvb::mi355x_part_tokens(shape, lens)):
+    a ragged batch caps max_part at 2048."""
+    lens = np.ascontiguousarray(lens, np.int32)
+    return host.kvbh_mi355x_part_tokens_lens(shape.batch, shape.num_heads, shape.num_kv_heads, shape.head_dim,
+                                             _ptr(lens), min_groups, min_part, max_part)
 
 
 def mi355x_min_groups(kv_type) -> int:
@@ -506,7 +515,7 @@ CONFIGS = {
 def config_part(cfg, w) -> int:
     """The partition tokens a configuration runs with (its own number, or the MI355X policy for w)."""
     if cfg["part"] == "mi355x":
-        return mi355x_part_tokens(w.shape, w.max_len, min_groups=mi355x_min_groups(w.kv_type))
+        return mi355x_part_tokens_for(w.shape, w.lens, min_groups=mi355x_min_groups(w.kv_type))
     return cfg["part"]
 
 

@@ -2,6 +2,7 @@
 // mirror, argument translation, and the reference's exceptions (src/metal_attn.mm:57-59, 134-293).
 #include "kvb/hip_attn.hpp"
 
+#include <algorithm>
 #include <cstring>
 #include <stdexcept>
 #include <string>
@@ -125,6 +126,17 @@ int mi355x_part_tokens(const Shape& s, int max_len, int min_groups, int min_part
     int part = max_part;
     while (part > min_part && per_part * ((max_len + part - 1) / part) < min_groups) part /= 2;
     return part;
+}
+
+int mi355x_part_tokens(const Shape& s, std::span<const int> lens, int min_groups, int min_part, int max_part) {
+    int max_len = 0;
+    bool ragged = false;
+    for (int len : lens) {
+        max_len = std::max(max_len, len);
+        ragged = ragged || len != lens[0];
+    }
+    if (ragged) max_part = std::max(min_part, std::min(max_part, kRaggedMaxPart));
+    return mi355x_part_tokens(s, max_len, min_groups, min_part, max_part);
 }
 
 kvb_paged_args c_args(const PagedArgs& a) {

@@ -197,6 +197,14 @@ int kvbh_poison_paged(int batch, int num_kv_heads, int head_dim, int page_size, 
     });
 }
 
+int kvbh_mi355x_part_tokens_lens(int batch, int num_heads, int num_kv_heads, int head_dim, const int* lens,
+                                 int min_groups, int min_part, int max_part) {
+    if (batch < 0 || (batch > 0 && !lens) || num_heads <= 0 || num_kv_heads <= 0 || min_part <= 0 || max_part < min_part)
+        return -1;
+    return kvb::mi355x_part_tokens(shape(batch, num_heads, num_kv_heads, head_dim), std::span<const int>(lens, size_t(batch)),
+                                   min_groups, min_part, max_part);
+}
+
 int kvbh_mi355x_part_tokens(int batch, int num_heads, int num_kv_heads, int head_dim, int max_len, int min_groups,
                             int min_part, int max_part) {
     if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || min_part <= 0 || max_part < min_part) return -1;

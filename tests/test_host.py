@@ -80,6 +80,15 @@ def test_mi355x_partition_policy(kvb):
     # c3 (B 16, 32/8 heads, 8k): 16 * 8 workgroups per partition
     assert kvb.mi355x_part_tokens(kvb.Shape(16, 32, 8, 128), 8192) == 4096
     assert kvb.mi355x_part_tokens(kvb.Shape(16, 32, 8, 128), 8192, min_groups=512) == 2048
+    # a ragged batch (lengths not all equal) caps the partition at 2048: c5's lengths -> 2048,
+    # c4's equal lengths keep 4096; an all-empty batch gets the floor
+    c5 = kvb.Shape(72, 32, 8, 128)
+    assert kvb.mi355x_part_tokens_for(c5, kvb.c5_lengths()) == 2048
+    assert kvb.mi355x_part_tokens_for(kvb.Shape(4, 64, 8, 128), [32768] * 4) == 4096
+    assert kvb.mi355x_part_tokens_for(kvb.Shape(2, 64, 8, 128), [32768, 100]) == 2048
+    assert kvb.mi355x_part_tokens_for(kvb.Shape(3, 8, 2, 64), [0, 0, 0]) == 256
+    assert kvb.mi355x_part_tokens_for(c5, kvb.c5_lengths(), max_part=1024) == 1024
+    assert kvb.host.kvbh_mi355x_part_tokens_lens(2, 8, 2, 64, None, 256, 256, 4096) == -1
     # BASELINE names c1's and c2's partitions; the policy is used where it leaves the choice
     assert kvb.CONFIGS["c1"]["part"] == 128 and kvb.CONFIGS["c2"]["part"] == 512
     assert all(kvb.CONFIGS[n]["part"] == "mi355x" for n in ("c3", "c4", "c5f16", "c5i8"))
