@@ -212,6 +212,8 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline(kvb, graft.load_oracle(), w, c)
         log(f"cpu baseline: {cpu['sample']}, {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['kind']})")
+        if devi is not None:  # the int8 cache too: dequantised (outside the timing), then the fp64 path
+            extras["int8_cpu_baseline"] = cpu_baseline(kvb, graft.load_oracle(), wi, ci)
 
     storage = {kvb.KV_F32: "f32", kvb.KV_F16: "f16", kvb.KV_I8: "i8"}[w.kv_type]
     line = {
