@@ -270,7 +270,10 @@ int kvb_device_name(char* buf, size_t cap) {
     if (int st = ensure_device()) return st;
     hipDeviceProp_t prop;
     KVB_HIP(hipGetDeviceProperties(&prop, g.device));
-    std::snprintf(buf, cap, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
+    if (prop.name[0])  // (the marketing name is empty on some systems: then the architecture leads)
+        std::snprintf(buf, cap, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
+    else
+        std::snprintf(buf, cap, "%s, %d CUs", prop.gcnArchName, prop.multiProcessorCount);
     return KVB_OK;
 }
 
