@@ -612,34 +612,55 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // ---- merge: lanes -> wave state -> workgroup
     const float vupf = KIND == KV_I8 ? ldexpf(1.0f, ve) : 1.0f;
     l = sum_x16_x32(l);
-    float* sacc = reinterpret_cast<float*>(vt);  // reuse the wave's V tile: [QG][D]
-    for (int mb = 0; mb < NMB; ++mb)
-        for (int i = 0; i < 4; ++i) {
-            const float o = (acc[mb][i] + dpp<kQuadSwap1>(acc[mb][i])) * vupf;  // high + low columns
-            if (hl == 0 && qcol) sacc[hh * D + 16 * mb + 4 * q4 + i] = o;
-        }
+    // The wave's accumulators go to its V tile as [QG][D] fp32: a high-column lane (hl == 0) holds
+    // d = 16 mb + 4 q4 + i (i < 4) of head hh, one 16-byte chunk per mb, and chunk c of head h's row
+    // is stored at c ^ (h & 7) so that the 8 heads' rows do not all start in the same LDS banks.
+    float* sacc = reinterpret_cast<float*>(vt);
+    for (int mb = 0; mb < NMB; ++mb) {
+        float4 o4;  // high + low columns
+        o4.x = (acc[mb][0] + dpp<kQuadSwap1>(acc[mb][0])) * vupf;
+        o4.y = (acc[mb][1] + dpp<kQuadSwap1>(acc[mb][1])) * vupf;
+        o4.z = (acc[mb][2] + dpp<kQuadSwap1>(acc[mb][2])) * vupf;
+        o4.w = (acc[mb][3] + dpp<kQuadSwap1>(acc[mb][3])) * vupf;
+        if (hl == 0 && qcol) *reinterpret_cast<float4*>(sacc + hh * D + 4 * ((4 * mb + q4) ^ (hh & 7))) = o4;
+    }
     if (hl == 0 && qcol && q4 == 0) s_ml[wave][hh] = make_float2(m, l);
     __syncthreads();
 
-    for (int idx = threadIdx.x; idx < QG * D; idx += 64 * W) {
-        const int h = idx / D, d = idx % D;
+    // The partition's result: thread e owns the 16-byte chunk ed of head eh. It weighs the waves'
+    // states once, sums them in wave order, and writes the chunk with one agent-scope (sc1) store,
+    // which writes through this XCD's L2 to the device coherence point, where the merging workgroup,
+    // on whichever XCD, reads it.
+    static_assert(QG * D / 4 <= 64 * W, "one 16-byte output chunk per thread");
+    if (threadIdx.x < QG * D / 4) {
+        const int eh = threadIdx.x / (D / 4), ed = threadIdx.x % (D / 4);
         float M = kNegBig;
-        for (int w = 0; w < W; ++w) M = fmaxf(M, s_ml[w][h].x);
-        float L = 0.0f, o = 0.0f;
+        for (int w = 0; w < W; ++w) M = fmaxf(M, s_ml[w][eh].x);
+        float L = 0.0f;
+        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         for (int w = 0; w < W; ++w) {
-            const float wt = __builtin_amdgcn_exp2f(s_ml[w][h].x - M);
-            L += s_ml[w][h].y * wt;
-            o += reinterpret_cast<const float*>(s_v[w])[h * D + d] * wt;
+            const float wt = __builtin_amdgcn_exp2f(s_ml[w][eh].x - M);
+            L += s_ml[w][eh].y * wt;
+            const float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(s_v[w]) + eh * D +
+                                                              4 * (ed ^ (eh & 7)));
+            o.x = __builtin_fmaf(v.x, wt, o.x);
+            o.y = __builtin_fmaf(v.y, wt, o.y);
+            o.z = __builtin_fmaf(v.z, wt, o.z);
+            o.w = __builtin_fmaf(v.w, wt, o.w);
         }
-        const size_t slot = ((size_t)b * H + h0 + h) * p.max_parts + part;
-        // Agent-scope stores (sc1) write through this XCD's L2 to the device coherence point, where
-        // the merging workgroup, on whichever XCD, reads them.
-        store_agent(p.part_out + slot * D + d, o / L);
-        if (d == 0) {
+        const float4 r = make_float4(o.x / L, o.y / L, o.z / L, o.w / L);
+        const size_t slot0 = ((size_t)b * H + h0) * p.max_parts + part;  // head h0's slot
+        const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(
+            p.part_out + slot0 * D, (short)0, QG * p.max_parts * D * 4, 0x00020000);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, r), rpo,
+                                               (eh * p.max_parts * D + 4 * ed) * 4, 0, kScopeAgent);
+        if (ed == 0) {
+            const size_t slot = slot0 + (size_t)eh * p.max_parts;
             store_agent(&p.part_ml[slot].x, M * kLn2);
             store_agent(&p.part_ml[slot].y, L);
         }
-        if (p.out && len <= p.part_tokens) p.out[((size_t)b * H + h0 + h) * D + d] = o / L;  // one partition
+        if (p.out && len <= p.part_tokens)  // one partition: this is the output
+            *reinterpret_cast<float4*>(p.out + ((size_t)b * H + h0 + eh) * D + 4 * ed) = r;
     }
     if (!p.out || len <= p.part_tokens) return;
 
@@ -668,7 +689,6 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // LDS (the V tiles are free again); then w_i replaces l_i; then the sums, in partition order,
     // with any partitions past kPre in batches of kBatch.
     static_assert(sizeof(s_v) / sizeof(float2) == fused_merge_slots(KIND, D), "merge staging size");
-    static_assert(QG * D / 4 <= 64 * W, "one 16-byte output chunk per thread");
     constexpr int kPre = 16, kBatch = 8;
     float2* s_pml = reinterpret_cast<float2*>(&s_v[0][0]);  // [QG][nparts]
     const size_t gbase = ((size_t)b * H + h0) * p.max_parts;  // first slot of head h0
