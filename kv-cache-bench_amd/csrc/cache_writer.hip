@@ -47,6 +47,21 @@ __device__ __forceinline__ uint32_t quantize_byte(float x, float scale) {
     return (uint32_t)(uint8_t)(int8_t)(int)q;
 }
 
+__device__ __forceinline__ float abs_max4(float m, const float4& v) {
+    return fmaxf(fmaxf(m, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+__device__ __forceinline__ uint32_t quantize4(const float4& v, float scale) {
+    if (!(scale > 0.0f)) return 0u;  // an all-zero slice: every byte 0
+    return quantize_byte(v.x, scale) | quantize_byte(v.y, scale) << 8 | quantize_byte(v.z, scale) << 16 |
+           quantize_byte(v.w, scale) << 24;
+}
+
+// A block of up to kWriterThreads * kQuantRegs groups of 4 values (page 128 at head_dim 128) is
+// read once and kept in registers between the max and the quantisation; a larger one is read twice,
+// the second time from L2.
+constexpr int kQuantRegs = 16;
+
 __global__ __launch_bounds__(kWriterThreads) void quantize_kernel(CacheWriteParams p) {
     const int kvh = blockIdx.x, b = blockIdx.y, blk_i = blockIdx.z;
     const int len = p.seq_lens[b], t0 = blk_i * p.page_size;
@@ -55,25 +70,31 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_kernel(CacheWritePara
     const size_t n4 = (size_t)rows * p.head_dim / 4;  // groups of 4 values (head_dim % 4 == 0)
     const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(p.contig) +
                                                         (((size_t)b * p.num_kv_heads + kvh) * p.max_len + t0) * p.head_dim);
-    float amax = 0.0f;
-    for (size_t w = threadIdx.x; w < n4; w += kWriterThreads) {
-        const float4 v = src[w];
-        amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
-    }
-    const float scale = block_max(amax) / 127.0f;
     const size_t blk = (size_t)p.block_table[(size_t)b * p.max_blocks + blk_i];
-    if (threadIdx.x == 0) p.scales[blk * p.num_kv_heads + kvh] = scale;
     uint32_t* dst = reinterpret_cast<uint32_t*>(static_cast<int8_t*>(p.paged) +
                                                 (blk * p.num_kv_heads + kvh) * p.page_size * p.head_dim);
-    for (size_t w = threadIdx.x; w < n4; w += kWriterThreads) {
-        uint32_t packed = 0;
-        if (scale > 0.0f) {
-            const float4 v = src[w];
-            packed = quantize_byte(v.x, scale) | quantize_byte(v.y, scale) << 8 | quantize_byte(v.z, scale) << 16 |
-                     quantize_byte(v.w, scale) << 24;
+    float amax = 0.0f;
+    if (n4 <= (size_t)kWriterThreads * kQuantRegs) {  // uniform over the workgroup
+        float4 v[kQuantRegs];
+#pragma unroll
+        for (int r = 0; r < kQuantRegs; ++r) {
+            const size_t w = threadIdx.x + (size_t)r * kWriterThreads;
+            v[r] = w < n4 ? src[w] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            amax = abs_max4(amax, v[r]);
         }
-        dst[w] = packed;
+        const float scale = block_max(amax) / 127.0f;
+        if (threadIdx.x == 0) p.scales[blk * p.num_kv_heads + kvh] = scale;
+#pragma unroll
+        for (int r = 0; r < kQuantRegs; ++r) {
+            const size_t w = threadIdx.x + (size_t)r * kWriterThreads;
+            if (w < n4) dst[w] = quantize4(v[r], scale);
+        }
+        return;
     }
+    for (size_t w = threadIdx.x; w < n4; w += kWriterThreads) amax = abs_max4(amax, src[w]);
+    const float scale = block_max(amax) / 127.0f;
+    if (threadIdx.x == 0) p.scales[blk * p.num_kv_heads + kvh] = scale;
+    for (size_t w = threadIdx.x; w < n4; w += kWriterThreads) dst[w] = quantize4(src[w], scale);
 }
 
 }  // namespace
