@@ -15,9 +15,10 @@
 //    fp32. fp32 caches use v_mfma_f32_16x16x4_f32 on q and K as they are (columns 2h+1 are zero).
 //  * In that layout a lane holds 8 tokens of one column, which is exactly its share of the P^T
 //    operand of O^T = V^T P^T (v_mfma_f32_16x16x32_f16 over 32 tokens): p = exp2(s - m) never
-//    leaves the lane, split into high and low fp16 parts like q. V^T comes from LDS, where the
-//    wave stores the V tile row-major with a 16-byte-chunk XOR swizzle that keeps the transposed
-//    2-byte reads free of bank conflicts. int8 V is widened to exact fp16 on the way into LDS.
+//    leaves the lane, split into high and low fp16 parts like q. V^T comes from LDS through the
+//    transposing reads (ds_read_b64_tr_b16 / _b8): the wave stores the V tile row-major, as stored
+//    (int8 as bytes, widened to exact fp16 after the read), with a 16-byte-chunk XOR swizzle that
+//    spreads the rows one half-wave reads over all the banks.
 //  * K is loaded straight into the A-operand layout: lane l reads 16 bytes of token l%16, lanes l,
 //    l+16, l+32, l+48 cover 64 contiguous bytes of that row per instruction. The contraction order
 //    over d is free, so each storage type picks the d order its loads give and q matches (dslot).
@@ -25,10 +26,12 @@
 //    across the four row groups.
 //  * int8: K bytes become exact fp16 (x ^ 0x80 under a 0x64 exponent, minus 1152) for the MFMA; the
 //    per-(block, KV head) K scale multiplies the score and the V scale multiplies p (normalised by a
-//    power of two per partition so the fp16 split of p * v_scale stays out of the subnormal range).
+//    running power of two per wave so the fp16 split of p * v_scale stays out of the subnormal range).
 //  * With DecodeParams::out set, the merge of the partitions (paged_reduce's job) is fused: the
 //    last workgroup of a (sequence, head group) to finish, found with an agent-scope counter,
 //    merges them, so a decode step is one kernel.
+//  * A ragged batch runs in longest-first order (ragged_item): grid y enumerates its partitions,
+//    the largest first, and each wave finds its workgroup's (sequence, partition) from seq_lens.
 //  * Tokens past the partition end get weight 0 and never reach the arithmetic as data. With
 //    `FAST` (every 16-token half tile inside one page) the block id and scales are one scalar read
 //    per half tile and K/V come through a buffer resource sized to its live rows, so rows past the
