@@ -192,7 +192,8 @@ def main():
         extras["warm_gbps"] = round(bytes_step / (extras["warm_chain_us"] * 1e-6) / 1e9, 1)
     keep.append(dev)
     if devi is not None:
-        parti = kvb.mi355x_part_tokens(w.shape, wi.max_len, min_groups=kvb.mi355x_min_groups(kvb.KV_I8)) \
+        parti = kvb.mi355x_part_tokens(w.shape, wi.max_len,
+                                       min_groups=kvb.mi355x_min_groups(kvb.KV_I8, w.shape.head_dim)) \
             if args.part is None else args.part
         extras["int8_part"] = parti
         ti, _ = timed_steps(kvb, devi, parti, args.steps, args.warmup)

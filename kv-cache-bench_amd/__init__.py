@@ -176,9 +176,10 @@ def mi355x_part_tokens_for(shape, lens, min_groups=256, min_part=256, max_part=4
                                              _ptr(lens), min_groups, min_part, max_part)
 
 
-def mi355x_min_groups(kv_type) -> int:
-    """The policy's workgroup target for a storage type (kvb::mi355x_min_groups): 256 for every type."""
-    return 256
+def mi355x_min_groups(kv_type, head_dim=128) -> int:
+    """The policy's workgroup target (kvb::mi355x_min_groups): 256, or 512 when a K or V row is under
+    128 bytes (int8 at head_dim 64)."""
+    return 512 if ELEM_SIZE[kv_type] * head_dim < 128 else 256
 
 
 @dataclass
@@ -515,7 +516,7 @@ CONFIGS = {
 def config_part(cfg, w) -> int:
     """The partition tokens a configuration runs with (its own number, or the MI355X policy for w)."""
     if cfg["part"] == "mi355x":
-        return mi355x_part_tokens_for(w.shape, w.lens, min_groups=mi355x_min_groups(w.kv_type))
+        return mi355x_part_tokens_for(w.shape, w.lens, min_groups=mi355x_min_groups(w.kv_type, w.shape.head_dim))
     return cfg["part"]
 
 

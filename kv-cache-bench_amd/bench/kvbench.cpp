@@ -98,7 +98,7 @@ int main(int argc, char** argv) {
     // The BASELINE configurations (fixed lengths; c5's ragged batch is bench.py's).
     if (config == "c1") shape = {1, 32, 8, 128}, lens = {512}, pages = {16}, parts = {128}, types = {KvType::f32}, pool = 2.0, dist = Dist::normal;
     else if (config == "c2") shape = {8, 32, 8, 128}, lens = {4096}, pages = {16}, parts = {512}, types = {KvType::f16}, pool = 1.5, dist = Dist::normal;
-    else if (config == "c3") shape = {16, 32, 8, 128}, lens = {8192}, pages = {64}, parts = {mi355x_part_tokens({16, 32, 8, 128}, 8192, mi355x_min_groups(KvType::i8))}, types = {KvType::i8}, pool = 1.0, dist = Dist::normal;
+    else if (config == "c3") shape = {16, 32, 8, 128}, lens = {8192}, pages = {64}, parts = {mi355x_part_tokens({16, 32, 8, 128}, 8192, mi355x_min_groups(KvType::i8, 128))}, types = {KvType::i8}, pool = 1.0, dist = Dist::normal;
     else if (config == "c4") shape = {4, 64, 8, 128}, lens = {32768}, pages = {128}, parts = {mi355x_part_tokens({4, 64, 8, 128}, 32768)}, types = {KvType::f16}, pool = 1.25, dist = Dist::normal;
     else if (!config.empty()) {
         std::fprintf(stderr, "unknown config %s (c1..c4)\n", config.c_str());

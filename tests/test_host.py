@@ -73,6 +73,10 @@ def test_mi355x_partition_policy(kvb):
     # c4 (B 4, 64/8 heads, 32k): 4 * 8 workgroups per partition -> 256 at part 4096
     assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768) == 4096
     assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768, min_groups=kvb.mi355x_min_groups(kvb.KV_I8)) == 4096
+    # int8 at head_dim 64 (64-byte rows) asks for two workgroups per CU
+    assert [kvb.mi355x_min_groups(t, d) for t in (kvb.KV_F32, kvb.KV_F16, kvb.KV_I8) for d in (64, 128)] == \
+        [256, 256, 256, 256, 512, 256]
+    assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 64), 32768, min_groups=kvb.mi355x_min_groups(kvb.KV_I8, 64)) == 2048
     assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768, min_groups=512) == 2048
     assert kvb.mi355x_part_tokens(kvb.Shape(4, 64, 8, 128), 32768, min_groups=1024) == 1024
     # short or small: the floor
