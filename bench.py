@@ -57,6 +57,15 @@ def split_steps(kvb, dev, part, steps):
     return statistics.median(d for d, _ in out), statistics.median(r for _, r in out)
 
 
+def loads_only(kvb, dev, part, steps=10):
+    """The decode's loads alone (kvb_run_paged_loads), cold: the memory-traffic floor of the kernel."""
+    out = []
+    for _ in range(steps):
+        kvb.flush_gpu_caches()
+        out.append(dev.run_loads(part))
+    return statistics.median(out)
+
+
 def warm_chain(kvb, dev, part, steps=20):
     """Back-to-back steps with warm caches (one event pair around the chain)."""
     dev.run(part)
@@ -188,6 +197,8 @@ def main():
         ud, ur = split_steps(kvb, dev, part, 10)
         extras["unfused_decode_us"] = round(ud * 1e3, 2)
         extras["unfused_reduce_us"] = round(ur * 1e3, 2)
+        if c.page_size % 16 == 0 and part_res % 16 == 0:
+            extras["loads_only_us"] = round(loads_only(kvb, dev, part) * 1e3, 2)
         extras["warm_chain_us"] = round(warm_chain(kvb, dev, part) * 1e3, 2)
         extras["warm_gbps"] = round(bytes_step / (extras["warm_chain_us"] * 1e-6) / 1e9, 1)
     keep.append(dev)
@@ -201,6 +212,8 @@ def main():
         extras["int8_us_per_step"] = round(medi * 1e3, 2)
         extras["int8_gbps"] = round(wi.min_bytes() / (medi * 1e-3) / 1e9, 1)
         extras["int8_speedup_vs_fp16"] = round(med / medi, 3)
+        if not args.no_extras:
+            extras["int8_loads_only_us"] = round(loads_only(kvb, devi, parti) * 1e3, 2)
         keep.append(devi)
         log(f"int8 c4-shape: {medi * 1e3:.1f} us ({extras['int8_speedup_vs_fp16']}x fp16)")
     if not args.no_extras:

@@ -154,6 +154,10 @@ struct KernelTimes {
 };
 KernelTimes run_paged_split(const PagedArgs&);
 
+// The decode's loads alone (kvb_run_paged_loads; not in the reference): every K/V and scale load of
+// paged_decode in the same order, no arithmetic, output not written. Returns GPU milliseconds.
+double run_paged_loads(const PagedArgs&);
+
 // Between begin_pipelined() and end_pipelined(), run_*() and flush_gpu_caches() queue their work
 // without waiting (run_*() return 0); end_pipelined() waits and returns the GPU time of every
 // run_*() call in order (src/metal_attn.hpp:93-99). On one HIP stream the runs execute one at a

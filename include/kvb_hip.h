@@ -112,6 +112,13 @@ int kvb_run_paged_steps(const kvb_paged_args* a, int steps, double* ms);
  * *reduce_ms are the hipEvent times of paged_decode (no merge) and of paged_reduce. Not in the
  * reference (its timing is per command buffer, src/metal_attn.mm:119-130). */
 int kvb_run_paged_split(const kvb_paged_args* a, double* decode_ms, double* reduce_ms);
+/* Measurement aid, not in the reference: the paged_decode launch of kvb_run_paged_split with the
+ * arithmetic taken out. Same grid and work order; every K/V load (and, for I8, every scale load)
+ * is issued in the same order and the registers are consumed by XORs. The output is not written
+ * (the library's workspace is scratch, as always). *ms = its hipEvent time: the time of
+ * the decode's memory traffic alone, which bounds the decode kernel from below. Same refusals as
+ * kvb_run_paged, plus KVB_EINVAL unless page_size and the partition are multiples of 16. */
+int kvb_run_paged_loads(const kvb_paged_args* a, double* ms);
 
 /* ---- cache writers on the GPU --------------------------------------------------------------
  * The producers of the paged cache the decode reads, as the reference runs them on the host:

@@ -89,6 +89,7 @@ _SIGS = {
     "kvb_run_paged": ([_PA, _d], _i),
     "kvb_run_paged_steps": ([_PA, _i, _d], _i),
     "kvb_run_paged_split": ([_PA, _d, _d], _i),
+    "kvb_run_paged_loads": ([_PA, _d], _i),
     "kvb_run_naive": ([_NA, _d], _i),
     "kvb_check_naive": ([_NA], _i),
     "kvb_run_attention_fp64": ([_NA, _d], _i),
@@ -404,6 +405,14 @@ class DeviceCase:
         a = self.args(part_tokens)
         check(hip.kvb_run_paged_split(ctypes.byref(a), ctypes.byref(d), ctypes.byref(r)), "run_paged_split")
         return d.value, r.value
+
+    def run_loads(self, part_tokens=0):
+        """The decode's loads alone (kvb_run_paged_loads): GPU ms of paged_decode's memory traffic
+        with no arithmetic; the output is not written."""
+        ms = ctypes.c_double()
+        a = self.args(part_tokens)
+        check(hip.kvb_run_paged_loads(ctypes.byref(a), ctypes.byref(ms)), "run_paged_loads")
+        return ms.value
 
     def output(self):
         s = self.w.shape

@@ -3,6 +3,7 @@
 // step; caches are flushed (1 GiB streaming read) before every timed run unless --no-flush; runs are
 // queued back to back (pipelined) unless --sync; the median of --reps runs is reported.
 // --chain=N times N back-to-back steps per submission with warm caches (run_paged_steps).
+// --loads adds a gpu_paged_loads row: the decode's loads alone, no arithmetic (run_paged_loads).
 // --bw runs the read-bandwidth probe. --config=c1..c4 selects a BASELINE configuration (N(0,1)
 // data, its page, partition and pool). --accuracy instead prints the error of the paged kernel for
 // each storage type against the fp64 attention of the unrounded fp32 data; --dump=DIR writes the
@@ -53,7 +54,7 @@ int main(int argc, char** argv) {
     std::vector<int> lens{512, 1024, 2048, 4096, 8192, 16384, 32768}, pages{16, 32, 64, 128}, parts{0};
     std::vector<KvType> types{KvType::f32, KvType::f16, KvType::i8};
     int reps = 30, warmup = 3, chain = 0;
-    bool naive = true, flush = true, per_head = false, bw = false, sync = false, accuracy = false;
+    bool naive = true, flush = true, per_head = false, bw = false, sync = false, accuracy = false, loads = false;
     std::string dump;
     Dist dist = Dist::uniform;
     double pool = 1.0;
@@ -86,6 +87,7 @@ int main(int argc, char** argv) {
         } else if (!std::strcmp(a, "--no-naive")) naive = false;
         else if (!std::strcmp(a, "--no-flush")) flush = false;
         else if (!std::strcmp(a, "--per-head")) per_head = true;
+        else if (!std::strcmp(a, "--loads")) loads = true;
         else if (!std::strcmp(a, "--bw")) bw = true;
         else if (!std::strcmp(a, "--sync")) sync = true;
         else if (!std::strcmp(a, "--accuracy")) accuracy = true;
@@ -246,6 +248,9 @@ int main(int argc, char** argv) {
                     const double diff = naive && !i8 ? max_abs_diff(out_paged.as<float>(), out_naive.as<float>(), n) : NAN;
                     const int p = part ? part : auto_part_tokens(w.shape, w.max_len);
                     row("gpu_paged", w, page, p, s, kt, diff, cache.bytes());
+                    if (loads && page % 16 == 0 && p % 16 == 0)
+                        row("gpu_paged_loads", w, page, p, time_gpu([&] { return run_paged_loads(cache.args(w, part, out_paged)); }),
+                            {}, NAN, cache.bytes());
                     if (per_head) {
                         PagedArgs args = cache.args(w, part, out_paged);
                         args.share_kv = false;

@@ -157,20 +157,28 @@ __global__ __launch_bounds__(256) void attention_fp64_kernel(NaiveParams p, int 
 // buffer of the probe (all words equal) produces.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(256) void read_bw_kernel(const u32x4_t* __restrict__ src, size_t n16, float* sink) {
-    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const size_t stride = (size_t)gridDim.x * 256;
+// Workgroup g reads the contiguous words [g * per_group, (g + 1) * per_group), kReadBwThreads at a
+// time, kReadBwUnroll loads in flight per thread (32 KB per workgroup).
+__global__ __launch_bounds__(kReadBwThreads) void read_bw_kernel(const u32x4_t* __restrict__ src, size_t n16,
+                                                                 size_t per_group, float* sink) {
+    const size_t beg = (size_t)blockIdx.x * per_group;
+    const size_t end = beg + per_group < n16 ? beg + per_group : n16;
+    constexpr int T = kReadBwThreads, U = kReadBwUnroll;
+    size_t i = beg + threadIdx.x;
     uint32_t acc = 0;
-    for (; i + 7 * stride < n16; i += 8 * stride) {
-        u32x4_t x[8];
-        for (int u = 0; u < 8; ++u) x[u] = __builtin_nontemporal_load(src + i + u * stride);
-        for (int u = 0; u < 8; ++u) acc ^= x[u].x ^ x[u].y ^ x[u].z ^ x[u].w;
+    for (; i + (U - 1) * T < end; i += U * T) {
+        u32x4_t x[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) x[u] = __builtin_nontemporal_load(src + i + u * T);
+        __builtin_amdgcn_sched_barrier(0);  // all U loads go out before the first wait
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= x[u].x ^ x[u].y ^ x[u].z ^ x[u].w;
     }
-    for (; i < n16; i += stride) {
+    for (; i < end; i += T) {
         const u32x4_t x = __builtin_nontemporal_load(src + i);
         acc ^= x.x ^ x.y ^ x.z ^ x.w;
     }
-    if (acc == 0x9e3779b9u) sink[((size_t)blockIdx.x * 256 + threadIdx.x) % kReadBwSink] = 1.0f;
+    if (acc == 0x9e3779b9u) sink[((size_t)blockIdx.x * T + threadIdx.x) % kReadBwSink] = 1.0f;
 }
 
 __global__ __launch_bounds__(256) void fill_kernel(uint4* dst, size_t n16, uint32_t value) {
@@ -208,9 +216,11 @@ hipError_t launch_attention_fp64(int kind, int head_dim, int group, const NaiveP
     return hipGetLastError();
 }
 
-hipError_t launch_read_bw(const void* src, size_t n16, float* sink, hipStream_t s, const Marks& m) {
-    // 32768 workgroups: the fastest shape of a sweep over 512..32768 on MI355X (~7.0 TB/s)
-    launch_marked(read_bw_kernel, dim3(kReadBwGroups), dim3(256), s, m, static_cast<const u32x4_t*>(src), n16, sink);
+hipError_t launch_read_bw(const void* src, size_t n16, int groups, float* sink, hipStream_t s, const Marks& m) {
+    if (groups <= 0) return hipErrorInvalidValue;
+    const size_t per_group = (n16 + groups - 1) / groups;
+    launch_marked(read_bw_kernel, dim3(groups), dim3(kReadBwThreads), s, m, static_cast<const u32x4_t*>(src), n16,
+                  per_group, sink);
     return hipGetLastError();
 }
 

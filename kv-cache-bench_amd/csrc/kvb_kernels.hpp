@@ -48,6 +48,9 @@ struct DecodeParams {
     // ragged_item in paged_decode_impl.hpp) instead of grid (y, z) = (sequence, partition).
     // Requires batch <= kRaggedMaxBatch and part_tokens < 65536.
     int ragged_items;
+    // Nonzero: launch the measurement variant that issues the decode's loads and computes nothing
+    // (tile-aligned pages only: page_size and part_tokens multiples of kTile).
+    int loads_only;
 };
 
 // Ragged batches up to this many sequences use the longest-first work order (one lane per
@@ -102,12 +105,17 @@ struct Marks {
 };
 
 template <typename... KArgs, typename... Args>
+inline void launch_marked_lds(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                              const Marks& m, Args... args) {
+    if (m.start || m.stop)
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, s, m.start, m.stop, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+}
+template <typename... KArgs, typename... Args>
 inline void launch_marked(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t s, const Marks& m,
                           Args... args) {
-    if (m.start || m.stop)
-        hipExtLaunchKernelGGL(kernel, grid, block, 0, s, m.start, m.stop, 0, args...);
-    else
-        hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
+    launch_marked_lds(kernel, grid, block, 0, s, m, args...);
 }
 
 // paged_decode for one storage kind: grid (H / qg, batch, max_parts), or (H / qg, ragged_items, 1)
@@ -150,11 +158,16 @@ hipError_t launch_write_paged(const CacheWriteParams& p, int batch, int max_bloc
 hipError_t launch_attention_fp64(int kind, int head_dim, int group, const NaiveParams& p, int batch, hipStream_t s,
                                  const Marks& m = {});
 
-// Streaming read of n16 16-byte words over kReadBwGroups workgroups; the guarded store into sink
-// (kReadBwSink floats) never fires for real data.
-constexpr int kReadBwGroups = 32768;
+// Streaming read of n16 16-byte words, one contiguous chunk per workgroup; the guarded store into
+// sink (kReadBwSink floats) never fires for real data. Measured on MI355X (cold, one launch), one
+// workgroup per CU of 512 threads with 4 loads in flight each was the fastest shape of a sweep
+// (grid-stride over 512..131072 workgroups, chunks over 256..8192 workgroups of 256..1024 threads,
+// 1..16 loads in flight) at every size tried: 7.15 TB/s on 537 MB, 7.20 on 1 GiB, 7.25 on 4 GiB,
+// against 6.56, 6.43 and 6.75-6.99 for 32768 workgroups x 256 threads x 8 grid-strided loads.
+constexpr int kReadBwThreads = 512;
+constexpr int kReadBwUnroll = 4;
 constexpr size_t kReadBwSink = 2048 * 256;
-hipError_t launch_read_bw(const void* src, size_t n16, float* sink, hipStream_t s, const Marks& m = {});
+hipError_t launch_read_bw(const void* src, size_t n16, int groups, float* sink, hipStream_t s, const Marks& m = {});
 // Overwrites n16 16-byte words with `value`.
 hipError_t launch_fill(void* dst, size_t n16, uint32_t value, hipStream_t s);
 

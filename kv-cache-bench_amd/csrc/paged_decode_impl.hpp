@@ -39,6 +39,8 @@
 //    (any page size) and lanes past the end re-read the partition's first token and zero it.
 #pragma once
 
+#include <algorithm>
+
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -274,7 +276,9 @@ __device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int bat
 
 // (waves_per_eu(2): up to two waves per SIMD, two workgroups per CU, each wave keeping one tile in
 // flight while it computes another; the register budget that leaves is 256 per lane)
-template <int KIND, int D, int QG, bool FAST>
+// LOADS: the measurement variant (kvb_run_paged_loads). It issues every load of the decode in the
+// same order and consumes the registers with XORs, and computes and writes nothing.
+template <int KIND, int D, int QG, bool FAST, bool LOADS = false>
 __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(DecodeParams p) {
     using T = KvT<KIND, D>;
     using R = TileRegs<KIND, D>;
@@ -475,7 +479,19 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     floatx4_t acc[NMB];
     for (int mb = 0; mb < NMB; ++mb) acc[mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+    uint32_t lsink = 0;  // LOADS: what the tiles' registers XOR to
     auto compute_tile = [&](const R& r, int tt) {
+        if constexpr (LOADS) {
+            for (int h = 0; h < 2; ++h) {
+                for (int mm = 0; mm < T::KLOADS; ++mm) lsink ^= r.k[h][mm].x ^ r.k[h][mm].y ^ r.k[h][mm].z ^ r.k[h][mm].w;
+                for (int i = 0; i < NV; ++i) lsink ^= r.v[h][i].x ^ r.v[h][i].y ^ r.v[h][i].z ^ r.v[h][i].w;
+            }
+            if constexpr (KIND == KV_I8)
+                for (int j = 0; j < 2; ++j)
+                    lsink ^= __builtin_bit_cast(uint32_t, r.ks[j]) ^ __builtin_bit_cast(uint32_t, r.vs[j]);
+            (void)tt;
+            return;
+        }
         store_v(r);
         // S^T = K Q^T for both halves
         floatx4_t S[2];
@@ -612,6 +628,11 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         }
     }
 
+    if constexpr (LOADS) {  // (never true for real data; keeps the loads live)
+        if (lsink == 0x9e3779b9u) p.part_out[threadIdx.x % D] = 1.0f;
+        return;
+    }
+
     // ---- merge: lanes -> wave state -> workgroup
     const float vupf = KIND == KV_I8 ? ldexpf(1.0f, ve) : 1.0f;
     l = sum_x16_x32(l);
@@ -742,10 +763,60 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Dynamic LDS for the loads-only variant so that a CU holds as many of its workgroups as of the
+// decode kernel's: the variant needs fewer registers and would otherwise run more workgroups per CU
+// whenever the grid has more than one per CU. The largest size at which the occupancy calculator
+// gives the variant the decode's count (at most what one workgroup may allocate); computed once per
+// instantiation.
+template <int KIND, int D, int QG>
+hipError_t loads_only_lds(size_t* lds) {
+    static size_t cached = SIZE_MAX;
+    if (cached == SIZE_MAX) {
+        const auto loads = paged_decode_kernel<KIND, D, QG, true, true>;
+        const int threads = 64 * decode_waves(KIND);
+        int occ = 0, dev = 0, lds_cu = 0, lds_wg = 0;
+        hipFuncAttributes fa{};
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, paged_decode_kernel<KIND, D, QG, true, false>,
+                                                                    threads, 0);
+        if (e == hipSuccess) e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_wg, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+        if (e == hipSuccess) e = hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(loads));
+        if (e != hipSuccess) return e;
+        size_t dyn = 0;
+        if (occ > 0) {
+            size_t per_group = std::min<size_t>((size_t)lds_cu / occ, (size_t)lds_wg) & ~size_t(255);
+            for (; per_group > fa.sharedSizeBytes; per_group -= 256) {
+                int got = 0;
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&got, loads, threads, per_group - fa.sharedSizeBytes);
+                if (e != hipSuccess) return e;
+                if (got >= occ) {
+                    dyn = per_group - fa.sharedSizeBytes;
+                    break;
+                }
+            }
+        }
+        cached = dyn;
+    }
+    *lds = cached;
+    return hipSuccess;
+}
+
 template <int KIND, int D, int QG, bool FAST>
 hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
     const dim3 grid(p.num_heads / QG, p.ragged_items ? p.ragged_items : batch, p.ragged_items ? 1 : p.max_parts);
-    launch_marked(paged_decode_kernel<KIND, D, QG, FAST>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
+    if (p.loads_only) {  // tile-aligned pages only
+        if constexpr (!FAST) {
+            return hipErrorInvalidValue;
+        } else {
+            size_t lds = 0;
+            if (const hipError_t e = loads_only_lds<KIND, D, QG>(&lds); e != hipSuccess) return e;
+            launch_marked_lds(paged_decode_kernel<KIND, D, QG, true, true>, grid, dim3(64 * decode_waves(KIND)), lds, s,
+                              m, p);
+        }
+    } else {
+        launch_marked(paged_decode_kernel<KIND, D, QG, FAST>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
+    }
     return hipGetLastError();
 }
 

@@ -42,6 +42,7 @@ struct Runtime {
     void* scores = nullptr;         // naive scores (grow-only)
     size_t scores_bytes = 0;
     void* flush_buf = nullptr;      // cache-flush source
+    int cus = 0;                    // compute units: the read probe runs one workgroup per CU
     float* sink = nullptr;          // read-probe sink
     bool pipelined = false;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> timed;
@@ -57,6 +58,7 @@ int ensure_device() {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(KVB_ENODEV, "no HIP device");
     KVB_HIP(hipGetDevice(&g.device));
+    KVB_HIP(hipDeviceGetAttribute(&g.cus, hipDeviceAttributeMultiprocessorCount, g.device));
     KVB_HIP(hipStreamCreateWithFlags(&g.own, hipStreamNonBlocking));
     if (!g.stream) g.stream = g.own;
     g.ready = true;
@@ -195,7 +197,8 @@ int ragged_items(const kvb_paged_args* a, int part) {
     return equal || items > 65535 ? 0 : (int)items;
 }
 
-int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, bool fused, const StepMarks& mk) {
+int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, bool fused, const StepMarks& mk,
+                  bool loads_only = false) {
     const int part = resolve_part(a);
     const int qg = query_heads_per_group(a);
     kvbk::DecodeParams p{};
@@ -218,6 +221,7 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     p.qscale = (1.0f / std::sqrt((float)a->head_dim)) * 1.4426950408889634f;
     p.batch = a->batch;
     p.ragged_items = ragged_items(a, part);
+    p.loads_only = loads_only;
     // fused merge when the group's partition (m, l) pairs fit its LDS staging
     if (fused && qg * p.max_parts > kvbk::fused_merge_slots(a->kv_type, a->head_dim)) fused = false;
     if (fused) {
@@ -234,7 +238,7 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
         default: e = kvbk::launch_paged_decode_i8(a->head_dim, qg, fast, p, a->batch, g.stream, dm); break;
     }
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("paged_decode launch: ") + hipGetErrorString(e));
-    if (fused) return KVB_OK;
+    if (fused || loads_only) return KVB_OK;
     kvbk::ReduceParams r{part_out, part_ml, a->seq_lens, a->out, a->num_heads, p.max_parts, part};
     e = kvbk::launch_paged_reduce(a->head_dim, r, a->batch, g.stream, rm);
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("paged_reduce launch: ") + hipGetErrorString(e));
@@ -402,6 +406,26 @@ int kvb_run_paged_split(const kvb_paged_args* a, double* decode_ms, double* redu
     return KVB_OK;
 }
 
+int kvb_run_paged_loads(const kvb_paged_args* a, double* ms) {
+    if (ms) *ms = 0.0;
+    if (int st = validate_paged(a)) return st;
+    const int part = resolve_part(a);
+    if (a->page_size % kvbk::kTile != 0 || part % kvbk::kTile != 0)
+        return fail(KVB_EINVAL, "the loads-only decode needs page_size and part_tokens that are multiples of 16");
+    if (int st = ensure_device()) return st;
+    if (a->batch == 0) return KVB_OK;
+    float* part_out = nullptr;
+    float2* part_ml = nullptr;
+    if (int st = workspace_for(a, &part_out, &part_ml)) return st;
+    hipEvent_t e0, e1;
+    if (int st = get_event(&e0)) return st;
+    if (int st = get_event(&e1)) return st;
+    StepMarks mk;
+    mk.decode = {e0, e1};
+    if (int st = enqueue_paged(a, part_out, part_ml, false, mk, true)) return st;
+    return finish(e0, e1, ms);
+}
+
 int kvb_check_write_paged(const kvb_cache_args* a) {
     if (!a) return fail(KVB_EINVAL, "null arguments");
     if (a->kv_type < KVB_KV_F32 || a->kv_type > KVB_KV_I8) return fail(KVB_EINVAL, "unknown kv_type");
@@ -534,7 +558,7 @@ int kvb_run_read_bandwidth(const void* dev, size_t bytes, double* ms) {
     hipEvent_t e0, e1;
     if (int st = get_event(&e0)) return st;
     if (int st = get_event(&e1)) return st;
-    const hipError_t e = kvbk::launch_read_bw(dev, bytes / 16, g.sink, g.stream, {e0, e1});
+    const hipError_t e = kvbk::launch_read_bw(dev, bytes / 16, g.cus, g.sink, g.stream, {e0, e1});
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("read_bw launch: ") + hipGetErrorString(e));
     return finish(e0, e1, ms);
 }
@@ -549,7 +573,7 @@ int kvb_flush_gpu_caches(void) {
         const hipError_t e = kvbk::launch_fill(g.flush_buf, kFlushBytes / 16, 0x3f800000u, g.stream);
         if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("flush fill: ") + hipGetErrorString(e));
     }
-    const hipError_t e = kvbk::launch_read_bw(g.flush_buf, kFlushBytes / 16, g.sink, g.stream);
+    const hipError_t e = kvbk::launch_read_bw(g.flush_buf, kFlushBytes / 16, g.cus, g.sink, g.stream);
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("flush launch: ") + hipGetErrorString(e));
     return KVB_OK;
 }

@@ -166,6 +166,15 @@ KernelTimes run_paged_split(const PagedArgs& a) {
     return t;
 }
 
+double run_paged_loads(const PagedArgs& a) {
+    kvb_paged_args c = view(a);
+    check(kvb_check_paged(&c), "run_paged_loads");
+    upload_inputs(a);
+    double ms = 0;
+    check(kvb_run_paged_loads(&c, &ms), "run_paged_loads");
+    return ms;
+}
+
 namespace {
 kvb_naive_args naive_view(const NaiveArgs& a) {
     kvb_naive_args c{};

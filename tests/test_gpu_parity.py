@@ -196,6 +196,27 @@ def test_steps_pipelined_and_deterministic(gpu):
     dev.free()
 
 
+@pytest.mark.parametrize("kv", ["f32", "f16", "i8"])
+def test_loads_only_decode(gpu, kv):
+    """kvb_run_paged_loads (the decode's loads, no arithmetic) runs on equal and ragged lengths,
+    reports a GPU time, leaves the output untouched, and a decode step afterwards is unchanged."""
+    kvb = gpu
+    for lens in ([2048, 2048, 2048], [2048, 17, 0]):
+        w = kvb.Workload(kvb.Shape(3, 32, 8, 128), kv, lens, seed=91)
+        c = kvb.PagedCache(w, 16, 5, pool_factor=1.5)
+        dev = kvb.DeviceCase(w, c)
+        dev.run(256)
+        want = dev.output()
+        dev.out.fill(0x7F)
+        sentinel = dev.output()
+        progress(f"[parity] loads-only {kv} lens {lens}")
+        assert dev.run_loads(256) > 0
+        assert np.array_equal(dev.output(), sentinel, equal_nan=True)
+        dev.run(256)
+        assert np.array_equal(dev.output(), want)
+        dev.free()
+
+
 def test_fused_merge_reads_fresh_partitions(gpu):
     """The fused merge reads partition results that other workgroups (other XCDs) wrote in the same
     launch. Two cases alternate through the library's one workspace and counter array, so a merge

@@ -135,6 +135,20 @@ class TestRefusals:
         ms = ctypes.c_double(-1)
         assert kvb.hip.kvb_run_paged(ctypes.byref(a), ctypes.byref(ms)) == kvb.KVB_EINVAL
         assert ms.value == 0.0
+        ms.value = -1
+        assert kvb.hip.kvb_run_paged_loads(ctypes.byref(a), ctypes.byref(ms)) == kvb.KVB_EINVAL
+        assert ms.value == 0.0
+
+    @pytest.mark.parametrize("kw", [dict(page_size=8, max_blocks=4), dict(part_tokens=24)])
+    def test_loads_only_needs_tile_aligned_pages(self, kvb, kw):
+        """kvb_run_paged_loads measures the tile-aligned decode only: a page or partition that is
+        not a multiple of 16 tokens is refused before any GPU work (kvb_run_paged accepts both)."""
+        a = self.args(kvb, **kw)
+        assert self.status(kvb, a) == kvb.KVB_OK
+        ms = ctypes.c_double(-1)
+        assert kvb.hip.kvb_run_paged_loads(ctypes.byref(a), ctypes.byref(ms)) == kvb.KVB_EINVAL
+        assert b"multiples of 16" in kvb.hip.kvb_last_error()
+        assert ms.value == 0.0
 
     def test_capacity_message_names_the_sequence(self, kvb):
         self.status(kvb, self.args(kvb, lens=[32, 33], max_len=64))
