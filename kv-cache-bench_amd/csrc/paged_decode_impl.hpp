@@ -708,10 +708,10 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
 
     // The merge is on the step's critical path (it starts when the last partition ends), so its
     // latency, not its few bytes, is what costs: one round trip for everything where possible.
-    // Thread e owns the 16-byte column chunk e of the group's [QG][D] output. It issues its rows
-    // of the first kPre partitions at once, together with the (m_i, l_i) of all partitions into
-    // LDS (the V tiles are free again); then w_i replaces l_i; then the sums, in partition order,
-    // with any partitions past kPre in batches of kBatch.
+    // Thread e owns the 16-byte column chunk e of the group's [QG][D] output. With more than kPre
+    // partitions, it issues its rows of the first kPre partitions at once, together with the
+    // (m_i, l_i) of all partitions into LDS (the V tiles are free again); then w_i replaces l_i;
+    // then the sums, in partition order, with the partitions past kPre in batches of kBatch.
     static_assert(sizeof(s_v) / sizeof(float2) == fused_merge_slots(KIND, D), "merge staging size");
     constexpr int kPre = 16, kBatch = 8;
     float2* s_pml = reinterpret_cast<float2*>(&s_v[0][0]);  // [QG][nparts]
@@ -724,8 +724,44 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                               rpo, ((eh * p.max_parts + i) * D + 4 * ed) * 4, 0, kScopeAgent));
     };
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float L = 0.0f;
+    auto add = [&](float wt, const float4& v) {
+        L += wt;
+        o.x = __builtin_fmaf(wt, v.x, o.x);
+        o.y = __builtin_fmaf(wt, v.y, o.y);
+        o.z = __builtin_fmaf(wt, v.z, o.z);
+        o.w = __builtin_fmaf(wt, v.w, o.w);
+    };
+    auto write_out = [&]() {
+        *reinterpret_cast<float4*>(p.out + ((size_t)b * H + h0 + eh) * D + 4 * ed) =
+            make_float4(o.x / L, o.y / L, o.z / L, o.w / L);
+    };
+    if (nparts <= kPre) {  // uniform
+        // Up to kPre partitions (every BASELINE configuration): each owner reads its head's (m_i, l_i)
+        // straight from the workspace together with its rows, so the merge is one round trip with
+        // no barrier. Same weights, same order as below.
+        if (owner) {
+            float4 pre[kPre];
+            float2 ml[kPre];
+            const size_t mslot = gbase + (size_t)eh * p.max_parts;
+            for (int j = 0; j < kPre; ++j)
+                if (j < nparts) {
+                    pre[j] = row(j);
+                    ml[j] = make_float2(load_agent(&p.part_ml[mslot + j].x), load_agent(&p.part_ml[mslot + j].y));
+                }
+            float M = kNegBig;
+            for (int j = 0; j < kPre; ++j)
+                if (j < nparts) M = fmaxf(M, ml[j].x);
+            for (int j = 0; j < kPre; ++j)
+                if (j < nparts) add(partition_weight(ml[j].x, ml[j].y, M), pre[j]);
+            write_out();
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     float4 pre[kPre];
-    for (int j = 0; j < kPre; ++j) pre[j] = row(j);  // slots past nparts are read and ignored
+    for (int j = 0; j < kPre; ++j) pre[j] = row(j);
     for (int x = threadIdx.x; x < QG * nparts; x += 64 * W) {
         const size_t slot = gbase + (size_t)(x / nparts) * p.max_parts + x % nparts;
         s_pml[x] = make_float2(load_agent(&p.part_ml[slot].x), load_agent(&p.part_ml[slot].y));
@@ -740,25 +776,14 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     __syncthreads();
     if (owner) {
         const float2* wrow = s_pml + eh * nparts;
-        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float L = 0.0f;
-        auto add = [&](float wt, const float4& v) {
-            L += wt;
-            o.x = __builtin_fmaf(wt, v.x, o.x);
-            o.y = __builtin_fmaf(wt, v.y, o.y);
-            o.z = __builtin_fmaf(wt, v.z, o.z);
-            o.w = __builtin_fmaf(wt, v.w, o.w);
-        };
-        for (int j = 0; j < kPre; ++j)
-            if (j < nparts) add(wrow[j].y, pre[j]);
+        for (int j = 0; j < kPre; ++j) add(wrow[j].y, pre[j]);
         for (int i0 = kPre; i0 < nparts; i0 += kBatch) {
             float4 v[kBatch];
             for (int j = 0; j < kBatch; ++j) v[j] = row(i0 + j);
             for (int j = 0; j < kBatch; ++j)
                 if (i0 + j < nparts) add(wrow[i0 + j].y, v[j]);
         }
-        *reinterpret_cast<float4*>(p.out + ((size_t)b * H + h0 + eh) * D + 4 * ed) =
-            make_float4(o.x / L, o.y / L, o.z / L, o.w / L);
+        write_out();
     }
     if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
