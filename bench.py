@@ -72,6 +72,16 @@ def warm_chain(kvb, dev, part, steps=20):
     return dev.run(part, steps=steps) / steps
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), and the core count the OS reports."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            name = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "unknown")
+    except OSError:
+        name = "unknown"
+    return f"{name}, {os.cpu_count()} logical CPUs"
+
+
 def cpu_baseline(kvb, oracle, w, c, seconds_budget=20.0):
     """The reference's fp64 attention (oracle/_ref when built, else this build's C oracle) on a bounded
     sample of the workload: the first non-empty sequence, all its heads, full context. int8 caches
@@ -104,6 +114,7 @@ def cpu_baseline(kvb, oracle, w, c, seconds_budget=20.0):
         "value": round(sample_bytes / med / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
+        "cpu": cpu_model(),
         "kind": "reference" if use_ref else "port",
         "sample": f"sequence {b} of {w.shape.batch} ({w.shape.num_heads} heads x {int(lens[0])} tokens), fp64 "
                   f"attention on the stored {'dequantised int8' if w.kv_type == kvb.KV_I8 else 'K/V'} values, "
