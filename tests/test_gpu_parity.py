@@ -265,3 +265,50 @@ def test_read_bandwidth_probe(gpu):
     progress(f"[parity] read probe 1 GiB: {gbps:.0f} GB/s")
     assert 500 < gbps < 12000
     buf.free()
+
+
+def random_case(i):
+    """Layout i of a fixed pseudo-random sweep: storage type, shape, lengths (with 0, 1 and tile,
+    page and partition edges mixed in), page size (tile-aligned or not), partition (automatic,
+    tile-aligned or not), pool size and scale variation."""
+    r = np.random.RandomState(1000 + i)
+    kv = ["f32", "f16", "i8"][i % 3]
+    hkv = int(r.choice([1, 2, 4, 8]))
+    g = int(r.choice([1, 2, 3, 4, 8]))
+    d = int(r.choice([64, 128]))
+    b = int(r.randint(1, 7))
+    page = int(r.choice([16, 32, 64, 128, 1, 3, 24, 48]))
+    part = int(r.choice([0, 16, 64, 256, 1024, 7, 100]))
+    edges = [0, 1, 15, 16, 17, 31, 32, 33, page, page + 1, max(part, 1), max(part, 1) + 1]
+    lens = [int(r.choice(edges)) if r.rand() < 0.4 else int(r.randint(0, 3000)) for _ in range(b)]
+    return kv, (b, hkv * g, hkv, d), lens, page, part, float(r.choice([1.0, 1.5, 3.0])), bool(r.rand() < 0.5)
+
+
+@pytest.mark.parametrize("i", range(30))
+def test_random_layouts(gpu, oracle, i):
+    """A fixed sweep of 30 layouts: the fused step against the oracle (tolerance) and against the
+    two-kernel step (bit for bit), with and without one workgroup per GQA group; where the
+    layout is tile-aligned, the loads-only variant runs too and leaves the output untouched."""
+    kvb = gpu
+    kv, shape, lens, page, part, pool, varied = random_case(i)
+    progress(f"[parity] random {i}: {kv} shape {shape} page {page} part {part} lens {lens}")
+    w = kvb.Workload(kvb.Shape(*shape), kv, lens, seed=2000 + i, varied=varied and kv == "i8")
+    c = kvb.PagedCache(w, page, 3000 + i, pool_factor=pool, poison=True)
+    dev = kvb.DeviceCase(w, c)
+    dev.out.fill(0xFF)
+    dev.run(part)
+    fused = dev.output()
+    pb.check_output(kvb, oracle, w, c, fused)
+    dev.out.fill(0xFF)
+    dev.run_split(part)
+    assert np.array_equal(dev.output(), fused)
+    dev.out.fill(0xFF)
+    dev.run(part, share_kv=False)
+    pb.check_output(kvb, oracle, w, c, dev.output())
+    eff = part if part else kvb.auto_part_tokens(w.shape.batch, w.shape.num_kv_heads, w.max_len)
+    if page % 16 == 0 and eff % 16 == 0:
+        dev.out.fill(0x7F)
+        sentinel = dev.output()
+        assert dev.run_loads(part) > 0
+        assert np.array_equal(dev.output(), sentinel)
+    dev.free()
