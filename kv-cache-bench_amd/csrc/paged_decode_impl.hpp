@@ -24,9 +24,12 @@
 //    over d is free, so each storage type picks the d order its loads give and q matches (dslot).
 //  * DPP quad swaps merge the high/low columns; lane shuffles reduce the tile max and the sums
 //    across the four row groups.
-//  * int8: K bytes become exact fp16 (x ^ 0x80 under a 0x64 exponent, minus 1152) for the MFMA; the
-//    per-(block, KV head) K scale multiplies the score and the V scale multiplies p (normalised by a
-//    running power of two per wave so the fp16 split of p * v_scale stays out of the subnormal range).
+//  * int8: the scores run on v_mfma_i32_16x16x64_i8 with K as stored and q split into three signed
+//    byte digits (q * 2^-e = d0 + d1 / 2^7 + d2 / 2^14): exact integer dot products per digit,
+//    combined in fp32. V bytes become exact fp16 (x ^ 0x80 under a 0x64 exponent, minus 1152) for the
+//    P*V MFMA. The per-(block, KV head) K scale multiplies the score and the V scale multiplies p
+//    (normalised by a running power of two per wave so the fp16 split of p * v_scale stays out of
+//    the subnormal range).
 //  * With DecodeParams::out set, the merge of the partitions (paged_reduce's job) is fused: the
 //    last workgroup of a (sequence, head group) to finish, found with an agent-scope counter,
 //    merges them, so a decode step is one kernel.
@@ -53,6 +56,7 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __fp16 fp16x8_t __attribute__((__vector_size__(8 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4_t;
@@ -404,8 +408,9 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     const bool qcol = hh < QG;
     const float* qp = p.q + ((size_t)b * H + h0 + (qcol ? hh : 0)) * D;
     float up = 1.0f;  // scores are MFMA results times `up` (a power of two)
-    half8_t aq16[F32 ? 1 : NJ];
+    half8_t aq16[KIND == KV_F16 ? NJ : 1];
     float aq32[F32 ? NJ : 1];
+    i32x4_t aq8[KIND == KV_I8 ? 2 * T::KLOADS : 1];  // int8: q digits, first and second score MFMA
     constexpr int QS = F32 ? 1 : 8;  // q elements per MFMA slot
     float qv[NJ][QS];                // raw loads only: any use before the barrier below would wait for them
     for (int j = 0; j < NJ; ++j)
@@ -437,17 +442,39 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         int e = 0;
         if (amax > 0.0f) {
             frexpf(amax, &e);  // amax < 2^e
-            e -= 14;           // the scaled q stays below 2^14, far from fp16 overflow
+            // fp16: the scaled q stays below 2^14, far from overflow; int8: below 2^7, a digit's range
+            e -= KIND == KV_I8 ? 7 : 14;
         }
         const float down = ldexpf(1.0f, -e);
         up = ldexpf(1.0f, e);
-        for (int j = 0; j < NJ; ++j)
-            for (int s = 0; s < 8; ++s) {
-                const float x = qv[j][s] * down;
-                const _Float16 hi = (_Float16)x;
-                const _Float16 lo = (_Float16)(x - (float)hi);
-                aq16[j][s] = hl ? lo : hi;
+        if constexpr (KIND == KV_F16) {
+            for (int j = 0; j < NJ; ++j)
+                for (int s = 0; s < 8; ++s) {
+                    const float x = qv[j][s] * down;
+                    const _Float16 hi = (_Float16)x;
+                    const _Float16 lo = (_Float16)(x - (float)hi);
+                    aq16[j][s] = hl ? lo : hi;
+                }
+        } else {
+            // int8 scores run on the integer MFMA, K as stored: x = q * down = d0 + d1 / 2^7 +
+            // d2 / 2^14 + err, |err| <= 2^-15, each digit a signed byte (every step is exact in
+            // fp32). Column 2h (hl == 0) carries d0 into the first MFMA and d2 into the second;
+            // column 2h + 1 carries d1 and zeros. Slot t of load m is d = 64 m + 16 q4 + t, as K's.
+            for (int m = 0; m < T::KLOADS; ++m) {
+                uint32_t wa[4] = {0u, 0u, 0u, 0u}, wb[4] = {0u, 0u, 0u, 0u};
+                for (int t = 0; t < 16; ++t) {
+                    const float x = qv[2 * m + (t >> 3)][t & 7] * down;
+                    const float d0 = fminf(fmaxf(__builtin_rintf(x), -127.0f), 127.0f);
+                    const float r1 = (x - d0) * 128.0f;
+                    const float d1 = fminf(fmaxf(__builtin_rintf(r1), -127.0f), 127.0f);
+                    const float d2 = fminf(fmaxf(__builtin_rintf((r1 - d1) * 128.0f), -127.0f), 127.0f);
+                    wa[t >> 2] |= (uint32_t)(uint8_t)(int8_t)(int)(hl ? d1 : d0) << (8 * (t & 3));
+                    wb[t >> 2] |= (hl ? 0u : (uint32_t)(uint8_t)(int8_t)(int)d2) << (8 * (t & 3));
+                }
+                aq8[m] = i32x4_t{(int)wa[0], (int)wa[1], (int)wa[2], (int)wa[3]};
+                aq8[T::KLOADS + m] = i32x4_t{(int)wb[0], (int)wb[1], (int)wb[2], (int)wb[3]};
             }
+        }
     }
 
     // ---- int8: p * v_scale is split into fp16 high and low parts for the P*V MFMA. It is
@@ -507,11 +534,15 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                 for (int j = 0; j < NJ; ++j)
                     S[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, r.k[h][j]), aq16[j], S[h], 0, 0, 0);
             } else {
-                for (int j = 0; j < NJ; ++j) {
-                    const uint4 w4 = r.k[h][j >> 1];
-                    const half8_t kb = (j & 1) ? i8x8_to_half8(w4.z, w4.w) : i8x8_to_half8(w4.x, w4.y);
-                    S[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb, aq16[j], S[h], 0, 0, 0);
+                // exact integer dot products per digit; the two scaled sums are the column's part
+                i32x4_t SA = {0, 0, 0, 0}, SB = {0, 0, 0, 0};
+                for (int m = 0; m < T::KLOADS; ++m) {
+                    const i32x4_t kk = __builtin_bit_cast(i32x4_t, r.k[h][m]);
+                    SA = __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, aq8[m], SA, 0, 0, 0);
+                    SB = __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, aq8[T::KLOADS + m], SB, 0, 0, 0);
                 }
+                const float wa = hl ? 1.0f / 128.0f : 1.0f, wb = hl ? 0.0f : 1.0f / 16384.0f;
+                for (int i = 0; i < 4; ++i) S[h][i] = __builtin_fmaf((float)SB[i], wb, (float)SA[i] * wa);
             }
         }
         if constexpr (KIND == KV_I8) {
