@@ -407,7 +407,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     const int hh = c >> 1, hl = c & 1;
     const bool qcol = hh < QG;
     const float* qp = p.q + ((size_t)b * H + h0 + (qcol ? hh : 0)) * D;
-    float up = 1.0f;  // scores are MFMA results times `up` (a power of two)
+    float up = 1.0f;  // scores are MFMA results times `up` (a power of two; int8: per head)
     half8_t aq16[KIND == KV_F16 ? NJ : 1];
     float aq32[F32 ? NJ : 1];
     i32x4_t aq8[KIND == KV_I8 ? 2 * T::KLOADS : 1];  // int8: q digits, first and second score MFMA
@@ -438,7 +438,15 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         float amax = 0.0f;
         for (int j = 0; j < NJ; ++j)
             for (int s = 0; s < 8; ++s) amax = fmaxf(amax, fabsf(qv[j][s]));
-        amax = wave_max(amax);
+        // fp16: one scale for the wave (floating point keeps each element's relative precision).
+        // int8: one per head, over the 8 lanes holding it (columns 2h, 2h + 1, all q4): the digits
+        // are fixed point, so a head with a small q next to a large one keeps its own precision.
+        if constexpr (KIND == KV_I8) {
+            amax = max_x16_x32(amax);
+            amax = fmaxf(amax, dpp<kQuadSwap1>(amax));
+        } else {
+            amax = wave_max(amax);
+        }
         int e = 0;
         if (amax > 0.0f) {
             frexpf(amax, &e);  // amax < 2^e

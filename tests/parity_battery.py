@@ -141,12 +141,19 @@ def check_gqa(kvb, oracle, run, shape):
     assert oracle.max_abs_diff(run(w, c, 256, True), want) <= tol
 
 
-def check_huge_and_tiny_queries(kvb, oracle, run):
-    """q far from 1 in magnitude: the fp16 high/low split scales q by a power of two first."""
-    w = kvb.Workload(kvb.Shape(2, 8, 2, 128), "f16", [500, 20], seed=51)
+def check_huge_and_tiny_queries(kvb, oracle, run, kv="f16"):
+    """q far from 1 in magnitude, over the whole query and per head inside one GQA group: the fp16
+    high/low split scales q by a power of two per wave, the int8 digits per head. With one scale
+    for the group, the 1.0 head's int8 digits would be fixed point on the 8000 head's scale."""
+    w = kvb.Workload(kvb.Shape(2, 8, 2, 128), kv, [500, 20], seed=51)
     c = kvb.PagedCache(w, 16, 3, poison=True)
-    for amp in (8000.0, 1e-3, 3e-6):
-        w.q[:] = np.random.Generator(np.random.PCG64(7)).uniform(-amp, amp, w.q.shape).astype(np.float32)
+    for amp in (8000.0, 1e-3, 3e-6, "mixed"):
+        rng = np.random.Generator(np.random.PCG64(7))
+        if amp == "mixed":  # the 4 heads of each group at 8000, 1, 1e-3 and 30
+            a = np.array([8000.0, 1.0, 1e-3, 30.0] * 2, np.float32)
+            w.q[:] = (rng.uniform(-1.0, 1.0, w.q.shape) * a[None, :, None]).astype(np.float32)
+        else:
+            w.q[:] = rng.uniform(-amp, amp, w.q.shape).astype(np.float32)
         want, tol = expected(kvb, oracle, w, c)
         assert oracle.max_abs_diff(run(w, c, 64, True), want) <= tol, amp
 

@@ -86,8 +86,9 @@ def test_gqa_groups(gpu, oracle, shape):
     pb.check_gqa(gpu, oracle, runner(gpu), shape)
 
 
-def test_huge_and_tiny_queries(gpu, oracle):
-    pb.check_huge_and_tiny_queries(gpu, oracle, runner(gpu))
+@pytest.mark.parametrize("kv", ["f32", "f16", "i8"])
+def test_huge_and_tiny_queries(gpu, oracle, kv):
+    pb.check_huge_and_tiny_queries(gpu, oracle, runner(gpu), kv)
 
 
 @pytest.mark.parametrize("kv", ["f32", "f16", "i8"])

@@ -49,8 +49,9 @@ def test_gqa_groups(kvb, oracle, model, shape):
     pb.check_gqa(kvb, oracle, model[0], shape)
 
 
-def test_huge_and_tiny_queries(kvb, oracle, model):
-    pb.check_huge_and_tiny_queries(kvb, oracle, model[0])
+@pytest.mark.parametrize("kv", ["f32", "f16", "i8"])
+def test_huge_and_tiny_queries(kvb, oracle, model, kv):
+    pb.check_huge_and_tiny_queries(kvb, oracle, model[0], kv)
 
 
 def test_storage_bounds_c2_f16(kvb, oracle, model):
