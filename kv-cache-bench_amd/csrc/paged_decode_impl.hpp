@@ -436,25 +436,37 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         for (int j = 0; j < NJ; ++j) aq32[j] = qv[j][0];
     } else {
         float amax = 0.0f;
+        bool finite = true;
         for (int j = 0; j < NJ; ++j)
-            for (int s = 0; s < 8; ++s) amax = fmaxf(amax, fabsf(qv[j][s]));
+            for (int s = 0; s < 8; ++s) {
+                const float a = fabsf(qv[j][s]);
+                amax = fmaxf(amax, a);
+                finite = finite && a <= 3.402823466e38f;
+            }
         // fp16: one scale for the wave (floating point keeps each element's relative precision).
         // int8: one per head, over the 8 lanes holding it (columns 2h, 2h + 1, all q4): the digits
         // are fixed point, so a head with a small q next to a large one keeps its own precision.
         if constexpr (KIND == KV_I8) {
+            if (!finite) amax = __builtin_inff();  // (the max carries it to the head's other lanes)
             amax = max_x16_x32(amax);
             amax = fmaxf(amax, dpp<kQuadSwap1>(amax));
         } else {
             amax = wave_max(amax);
         }
         int e = 0;
-        if (amax > 0.0f) {
+        if (amax > 0.0f && amax <= 3.402823466e38f) {
             frexpf(amax, &e);  // amax < 2^e
             // fp16: the scaled q stays below 2^14, far from overflow; int8: below 2^7, a digit's range
             e -= KIND == KV_I8 ? 7 : 14;
         }
-        const float down = ldexpf(1.0f, -e);
+        float down = ldexpf(1.0f, -e);
         up = ldexpf(1.0f, e);
+        if (KIND == KV_I8 && !(amax <= 3.402823466e38f)) {
+            // a NaN or infinite q element: the head's scores are NaN, as in floating point (the
+            // digits alone would clamp it to a finite value)
+            down = 0.0f;
+            up = __builtin_nanf("");
+        }
         if constexpr (KIND == KV_F16) {
             for (int j = 0; j < NJ; ++j)
                 for (int s = 0; s < 8; ++s) {

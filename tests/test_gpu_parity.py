@@ -313,3 +313,21 @@ def test_random_layouts(gpu, oracle, i):
         assert dev.run_loads(part) > 0
         assert np.array_equal(dev.output(), sentinel)
     dev.free()
+
+
+@pytest.mark.parametrize("kv", ["f32", "f16", "i8"])
+def test_non_finite_query_poisons_only_its_head(gpu, oracle, kv):
+    """A NaN (or infinite) element of one head's q makes that head's output NaN, as floating point
+    does, and leaves the other heads of its group exact to the tolerance."""
+    kvb = gpu
+    w = kvb.Workload(kvb.Shape(2, 8, 2, 128), kv, [300, 40], seed=61)
+    c = kvb.PagedCache(w, 16, 9, pool_factor=1.5, poison=True)
+    clean, tol = pb.expected(kvb, oracle, w, c)
+    for bad in (np.nan, np.inf):
+        w.q[0, 1, 17] = bad
+        got = run(kvb, w, c, 64)
+        assert np.isnan(got[0, 1]).all(), bad
+        keep = np.ones(got.shape[:2], bool)
+        keep[0, 1] = False
+        assert np.abs(got[keep] - clean[keep]).max() <= tol, bad
+        w.q[0, 1, 17] = 0.5
