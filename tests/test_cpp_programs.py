@@ -97,3 +97,36 @@ def test_kvbench_dump(gpu, oracle, tmp_path):
     assert oracle.max_abs_diff(ref32, want) <= 1e-6
     # the f16 dump is of the fp16-rounded values: close to, not equal to, the fp32 one
     assert 0 < oracle.max_abs_diff(ref16, ref32) < 1e-2
+
+
+@pytest.mark.gpu
+def test_kvbench_csv_and_loads(gpu):
+    """The default CSV (the reference's bench/bench.cpp:121-259 schema, plus decode/reduce split and
+    kv_bytes): gpu_naive and gpu_paged rows per (type, length, page, partition), the paged output
+    against the naive one, and --loads rows timed below the full step; --bw one read_bw row."""
+    out = subprocess.run([KVBENCH, "--batch=2", "--lens=2048", "--pages=16,64", "--parts=256", "--reps=3",
+                          "--warmup=1", "--loads", "--types=f32,f16,i8"],
+                         capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    lines = [r for r in out.stdout.splitlines() if r and not r.startswith("#")]
+    head = lines[0].split(",")
+    assert head[:11] == ["impl", "dtype", "batch", "seq_len", "page", "part", "reps", "median_us", "min_us",
+                         "max_us", "gbps"]
+    rows = [dict(zip(head, r.split(","))) for r in lines[1:]]
+    by = {}
+    for r in rows:
+        by.setdefault(r["impl"], []).append(r)
+    assert len(by["gpu_naive"]) == 2  # f32 and f16 (the naive kernels take no int8)
+    assert len(by["gpu_paged"]) == 3 * 2 and len(by["gpu_paged_loads"]) == 3 * 2
+    for r in by["gpu_paged"]:
+        if r["dtype"] != "i8":
+            assert float(r["max_diff_vs_naive"]) <= 2e-5, r
+    step = {(r["dtype"], r["page"]): float(r["median_us"]) for r in by["gpu_paged"]}
+    for r in by["gpu_paged_loads"]:
+        assert 0 < float(r["median_us"]) <= 1.5 * step[(r["dtype"], r["page"])], r
+    bw = subprocess.run([KVBENCH, "--bw", "--bw-bytes=268435456", "--reps=3"], capture_output=True, text=True,
+                        timeout=300)
+    assert bw.returncode == 0, bw.stderr
+    b = [r.split(",") for r in bw.stdout.splitlines() if r.startswith("read_bw,")]
+    assert len(b) == 1 and 500 < float(b[0][6]) < 12000
+    progress(f"[kvbench] paged f16 page 64: {step[('f16', '64')]} us; read_bw 256 MiB: {b[0][6]} GB/s")
