@@ -32,7 +32,10 @@
 //    the subnormal range).
 //  * With DecodeParams::out set, the merge of the partitions (paged_reduce's job) is fused: the
 //    last workgroup of a (sequence, head group) to finish, found with an agent-scope counter,
-//    merges them, so a decode step is one kernel.
+//    merges them, so a decode step is one kernel. Up to 16 partitions, each thread reads its
+//    head's (m, l) with its rows in one round trip; past that, the (m, l) go through LDS.
+//  * The LOADS instantiation (kvb_run_paged_loads) keeps every load and drops the arithmetic: the
+//    time of the decode's memory traffic alone, for measurement.
 //  * A ragged batch runs in longest-first order (ragged_item): grid y enumerates its partitions,
 //    the largest first, and each wave finds its workgroup's (sequence, partition) from seq_lens.
 //  * Tokens past the partition end get weight 0 and never reach the arithmetic as data. With
