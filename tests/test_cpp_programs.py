@@ -14,8 +14,8 @@ BIN = os.path.join(BUILD, "tests")
 
 def run(name, timeout):
     progress(f"[cpp] {name} starts")
-    log_dir = os.path.join(ROOT, "gpurun_out")
-    log = open(os.path.join(log_dir, f"{name}.log"), "w") if os.path.isdir(log_dir) else None
+    log_dir = os.environ.get("KVB_LOG_DIR")  # optional: keep each program's full output there
+    log = open(os.path.join(log_dir, f"{name}.log"), "w") if log_dir and os.path.isdir(log_dir) else None
     p = subprocess.Popen([os.path.join(BIN, name)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     lines = []
     for line in p.stdout:  # streamed, so a long run keeps showing progress
