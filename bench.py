@@ -82,46 +82,57 @@ def cpu_model():
     return f"{name}, {os.cpu_count()} logical CPUs"
 
 
-def cpu_baseline(kvb, oracle, w, c, seconds_budget=20.0):
-    """The reference's fp64 attention (oracle/_ref when built, else this build's C oracle) on a bounded
-    sample of the workload: the first non-empty sequence, all its heads, full context. int8 caches
-    are dequantised first (outside the timing), as the reference's PagedCache::reference does."""
+def cpu_baseline(kvb, oracle, w, c, seconds_budget=20.0, max_bytes=1 << 30):
+    """The reference's fp64 attention (oracle/_ref when built, else this build's C oracle), timed on
+    the whole step when its stored K/V fit in max_bytes (every configuration but the ragged c5), else
+    on the longest prefix of sequences that fits (at least one non-empty one): all heads, full
+    context. int8 caches are dequantised first (outside the timing), as the reference's
+    PagedCache::reference does."""
     threads = max(1, min(16, os.cpu_count() or 1))
-    b = next(i for i, L in enumerate(w.lens) if L > 0)
-    s1 = type(w.shape)(1, w.shape.num_heads, w.shape.num_kv_heads, w.shape.head_dim)
-    lens = w.lens[b:b + 1]
+    esz = {kvb.KV_F32: 4, kvb.KV_F16: 2, kvb.KV_I8: 1}[w.kv_type]
+    row = w.shape.num_kv_heads * w.shape.head_dim * esz * 2  # stored K + V bytes per token
+    n, tokens = 0, 0
+    for L in w.lens:
+        if tokens > 0 and (tokens + int(L)) * row > max_bytes:
+            break
+        n, tokens = n + 1, tokens + int(L)
+    full = n == w.shape.batch
+    sn = type(w.shape)(n, w.shape.num_heads, w.shape.num_kv_heads, w.shape.head_dim)
+    lens = w.lens[:n]
     if w.kv_type == kvb.KV_I8:
         kd, vd = c.dequantized(w)
-        k, v = kd[b:b + 1], vd[b:b + 1]
+        k, v = kd[:n], vd[:n]
     else:
-        k, v = w.k[b:b + 1], w.v[b:b + 1]
-    q = w.q[b:b + 1]
+        k, v = w.k[:n], w.v[:n]
+    q = w.q[:n]
     use_ref = oracle.ref is not None
     fn = oracle.ref_attention if use_ref else oracle.attention
-    fn(s1, lens, w.max_len, q, k, v, threads=threads)  # warm-up
+    fn(sn, lens, w.max_len, q, k, v, threads=threads)  # warm-up
     times = []
     t_start = time.perf_counter()
-    while len(times) < 3 and (time.perf_counter() - t_start) < seconds_budget:
+    while len(times) < 5 and (time.perf_counter() - t_start) < seconds_budget:
         t0 = time.perf_counter()
-        fn(s1, lens, w.max_len, q, k, v, threads=threads)
+        fn(sn, lens, w.max_len, q, k, v, threads=threads)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    esz = {kvb.KV_F32: 4, kvb.KV_F16: 2, kvb.KV_I8: 1}[w.kv_type]
-    sample_bytes = float(lens[0]) * w.shape.num_kv_heads * w.shape.head_dim * esz * 2 + \
-        w.shape.num_heads * w.shape.head_dim * 4 * 2
-    per_step = med * float(w.lens.sum()) / float(lens[0])
-    return {
+    sample_bytes = float(tokens) * row + n * w.shape.num_heads * w.shape.head_dim * 4 * 2
+    what = f"the whole step ({n} sequences, {tokens} tokens)" if full else \
+        f"sequences 0-{n - 1} of {w.shape.batch} ({tokens} of {int(w.lens.sum())} tokens)"
+    out = {
         "value": round(sample_bytes / med / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "cpu": cpu_model(),
         "kind": "reference" if use_ref else "port",
-        "sample": f"sequence {b} of {w.shape.batch} ({w.shape.num_heads} heads x {int(lens[0])} tokens), fp64 "
-                  f"attention on the stored {'dequantised int8' if w.kv_type == kvb.KV_I8 else 'K/V'} values, "
-                  f"median of {len(times)} runs after 1 warm-up: {med * 1e3:.1f} ms "
-                  f"(~{per_step * 1e3:.0f} ms per full step by token count)",
-        "ms_per_step_extrapolated": round(per_step * 1e3, 2),
+        "sample": f"{what} x {w.shape.num_heads} heads, fp64 attention on the stored "
+                  f"{'dequantised int8' if w.kv_type == kvb.KV_I8 else 'K/V'} values, median of {len(times)} "
+                  f"runs after 1 warm-up: {med * 1e3:.1f} ms",
     }
+    if full:
+        out["ms_per_step"] = round(med * 1e3, 2)
+    else:
+        out["ms_per_step_extrapolated"] = round(med * float(w.lens.sum()) / float(tokens) * 1e3, 2)
+    return out
 
 
 WORKLOAD_TEXT = {
