@@ -33,3 +33,21 @@ def test_status_codes_and_no_device_here(kvb):
     ptr = ctypes.c_void_p()
     assert kvb.hip.kvb_buffer_alloc(ctypes.byref(ptr), 64) == kvb.KVB_ENODEV
     assert b"no HIP device" in kvb.hip.kvb_last_error()
+
+
+def test_package_without_built_libraries_raises(tmp_path):
+    """No CPU fallback: with the libraries absent, importing the package fails loudly."""
+    import subprocess
+    import sys
+    code = ("import importlib.util, sys\n"
+            f"spec = importlib.util.spec_from_file_location('kvb', {os.path.join(ROOT, 'kv-cache-bench_amd', '__init__.py')!r})\n"
+            "m = importlib.util.module_from_spec(spec)\n"
+            "try:\n"
+            "    spec.loader.exec_module(m)\n"
+            "except ImportError as e:\n"
+            "    print('ImportError:', e); sys.exit(3)\n"
+            "sys.exit(0)\n")
+    env = dict(os.environ, KVB_BUILD_DIR=str(tmp_path))
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 3, r.stdout + r.stderr
+    assert "libkvb_hip.so is not built" in r.stdout
