@@ -56,3 +56,31 @@ def test_cpu_baseline_leg(kvb, oracle):
     wi = kvb.Workload(kvb.Shape(2, 8, 2, 128), "i8", [40, 0], seed=6)
     ci = kvb.PagedCache(wi, 16, 8)
     assert "dequantised int8" in bench.cpu_baseline(kvb, oracle, wi, ci, seconds_budget=5.0)["sample"]
+
+
+@pytest.mark.gpu
+def test_bench_line_contract(kvb):
+    """On a GPU: one JSON line with the driver's keys, the roofline object and a CPU baseline, and
+    numbers that agree with each other (c1 keeps it short)."""
+    import json
+    from conftest import progress
+    progress("[bench] c1 contract run")
+    r = subprocess.run([sys.executable, BENCH, "--config", "c1", "--steps", "5", "--warmup", "1", "--no-extras"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [l for l in r.stdout.splitlines() if l.strip()]
+    assert len(lines) == 1, r.stdout
+    d = json.loads(lines[0])
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+                "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
+        assert key in d, key
+    assert (d["n_gpus"], d["steps"], d["warmup"]) == (1, 5, 1)
+    assert d["unit"] == "GB/s" and d["higher_is_better"] is True and d["vs_baseline"] is None
+    rf = d["roofline"]
+    assert rf["bound"] == "hbm" and rf["peak"] == 8000.0 and rf["unit"] == "GB/s"
+    assert abs(rf["frac"] - rf["achieved"] / rf["peak"]) < 1e-3
+    assert rf["bytes_per_launch"] == d["config"]["bytes_per_step"]
+    assert abs(d["value"] - d["config"]["bytes_per_step"] / (d["ms_per_step"] * 1e-3) / 1e9) < 0.01 * d["value"]
+    cpu = d["cpu_baseline"]
+    assert cpu["value"] > 0 and cpu["cores"] >= 1 and cpu["kind"] in ("reference", "port")
+    assert cpu["sample"].startswith("the whole step")
