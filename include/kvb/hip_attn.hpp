@@ -9,7 +9,7 @@
 #include <string>
 #include <vector>
 
-#include "kvb/layout.hpp"
+#include "kvb/reference.hpp"
 #include "kvb_hip.h"
 
 namespace kvb {
@@ -56,7 +56,7 @@ inline const char* name(KvType t) { return t == KvType::f32 ? "f32" : t == KvTyp
 inline size_t elem_size(KvType t) { return t == KvType::f32 ? 4 : t == KvType::f16 ? 2 : 1; }
 
 // The reference's simdgroups per workgroup (src/metal_attn.hpp:41). Here paged_decode workgroups
-// have 4 wave64s for f32/f16 caches and 8 for int8.
+// have 4 wave64s, one per SIMD, for every storage type.
 constexpr int kSimdGroups = 4;
 
 // Split-K partition size used when PagedArgs::part_tokens is 0 (src/metal_attn.hpp:43-51): the

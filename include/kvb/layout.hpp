@@ -1,6 +1,6 @@
 // Shapes, the paged block table and the cache writers of the host layer (the layout half of the
-// reference's src/reference.hpp:11-81). The fp64 attention reference of that file is not part of
-// the product: it lives in oracle/ as test infrastructure and CPU baseline.
+// reference's src/reference.hpp:11-81). The fp64 attention reference of that file is declared in
+// kvb/reference.hpp and defined by the reference's own CPU code, not by this build's libraries.
 #pragma once
 
 #include <algorithm>

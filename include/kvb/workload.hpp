@@ -1,6 +1,7 @@
 // Random decode workloads shared by the tests and the benchmark (the reference's src/workload.hpp).
 #pragma once
 
+#include <cmath>
 #include <cstdint>
 #include <memory>
 #include <vector>
@@ -44,6 +45,18 @@ struct Workload {
     // (src/workload.hpp:68-74; int8 scales not included).
     double min_bytes() const;
 
+    // Fills `out` (out_floats() floats) with the fp64 attention reference on the contiguous cache:
+    // the stored fp16 values for f16, the unquantised fp32 values for f32 and i8
+    // (src/workload.hpp:76-83). attention_reference is the reference's own CPU code, linked by the
+    // caller (kvb/reference.hpp); nothing in this build's libraries calls this.
+    void reference(float* out, int threads = 1) const {
+        with_type(type, [&]<class T>(T) {
+            attention_reference<T>(shape, lens, max_len, static_cast<const float*>(q->host()),
+                                   static_cast<const T*>(k->host()), static_cast<const T*>(v->host()), out,
+                                   1.0f / std::sqrt(float(shape.head_dim)), threads);
+        });
+    }
+
     NaiveArgs naive_args(const Buffer& out) const;
 };
 
@@ -64,6 +77,19 @@ struct PagedCache {
     size_t bytes() const;
     // Bytes of the int8 scales of live blocks a decode step reads (0 for f32/f16).
     double scale_bytes(const Workload& w) const;
+
+    // fp64 reference on the values the kernel reads: the dequantised cache for i8, otherwise
+    // Workload::reference (src/workload.hpp:128-137).
+    void reference(const Workload& w, float* out, int threads = 1) const {
+        if (w.type != KvType::i8) return w.reference(out, threads);
+        std::vector<float> kd(w.k->size() / sizeof(float)), vd(kd.size());
+        dequantize_paged_i8(w.shape, layout, w.lens, w.max_len, static_cast<const int8_t*>(k->host()),
+                            static_cast<const float*>(k_scale->host()), kd.data());
+        dequantize_paged_i8(w.shape, layout, w.lens, w.max_len, static_cast<const int8_t*>(v->host()),
+                            static_cast<const float*>(v_scale->host()), vd.data());
+        attention_reference<float>(w.shape, w.lens, w.max_len, static_cast<const float*>(w.q->host()), kd.data(),
+                                   vd.data(), out, 1.0f / std::sqrt(float(w.shape.head_dim)), threads);
+    }
 
     PagedArgs args(const Workload& w, int part_tokens, const Buffer& out) const;
 };

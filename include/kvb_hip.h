@@ -37,10 +37,13 @@ int kvb_device_name(char* buf, size_t cap);
 /* Message of the last call that did not return KVB_OK ("" if none). */
 const char* kvb_last_error(void);
 /* Runs the library's work on `stream` (a hipStream_t; NULL = the library's own stream, created
- * at default priority). Timing events are recorded on the same stream. No reference counterpart:
- * lets a caller that owns a stream (a serving loop, PyTorch) order decode steps with its own work. */
+ * at default priority). Timing events are recorded on the same stream. Work queued on the new
+ * stream after this call waits for everything already queued on the previous one (an event), since
+ * every stream shares the library's workspace and merge counters: switching never lets two steps
+ * run at once. No reference counterpart: lets a caller that owns a stream (a serving loop,
+ * PyTorch) order decode steps with its own work. */
 int kvb_set_stream(void* stream);
-/* Waits for all work the library has queued. */
+/* Waits for all work the library has queued (on the current stream, which waits for the earlier ones). */
 int kvb_synchronize(void);
 
 /* ---- memory (Buffer, src/metal_attn.hpp:16-33) ------------------------------------------- */
@@ -71,7 +74,12 @@ typedef struct kvb_paged_args {
     const int32_t* block_table;  /* device, int32 [B][max_blocks]; logical block i of sequence b
                                     lives in physical block block_table[b*max_blocks + i] */
     const int32_t* seq_lens;     /* device, int32 [B] */
-    const int32_t* host_seq_lens;/* host copy of seq_lens, equal to it: capacity check, launch size */
+    const int32_t* host_seq_lens;/* host copy of seq_lens, equal to it: capacity check, launch size.
+                                    If the device copy disagrees, the kernels clamp each of its lengths
+                                    to [0, min(max_blocks * page_size, max_parts * part)] and read a -1
+                                    table entry as an empty page, so they stay inside the table rows and
+                                    the workspace; the output is then unspecified. Block ids themselves
+                                    are trusted (the pool's size is not an argument), as in the reference. */
     float* out;                  /* device, float [B][H][D] */
     const float* k_scale;        /* device, float [blocks][Hkv]; required for I8 */
     const float* v_scale;
@@ -98,9 +106,10 @@ int kvb_check_paged(const kvb_paged_args* a);
 
 /* One decode step (run_paged, src/metal_attn.hpp:86): the reference's paged_decode + paged_reduce
  * as one launch of paged_decode whose last workgroup per (sequence, KV-head group) merges the
- * partitions; two kernels (paged_decode, then paged_reduce) when a group's partition count
- * exceeds what that merge stages on chip (query heads per group x max_parts > 1024 for f16 at
- * head_dim 128, 2048 for i8 and f32; half that at head_dim 64). Either form gives the same bits. *ms = GPU time
+ * partitions; two kernels (paged_decode, then paged_reduce) when a group's (m, l) pairs exceed what
+ * that merge stages in LDS: query heads per group x max_parts > 4 waves x 32 tokens x head_dim x
+ * elem_size / 8 (at head_dim 128: 4096 for f16, 8192 for f32, 2048 for i8; half that at 64).
+ * Either form gives the same bits. *ms = GPU time
  * from before the first kernel to after the last (hipEvent pair); 0 in pipelined mode. Refuses (KVB_EINVAL, before any GPU work, output untouched) part_tokens < 0, max_len < 0,
  * page_size <= 0, I8 without scales, a length < 0 or > max_len or > max_blocks * page_size,
  * head_dim not 64/128, H % Hkv != 0 (src/metal_attn.mm:72-73, 107-117, 199-201). */

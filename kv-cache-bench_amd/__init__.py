@@ -490,6 +490,12 @@ def synchronize():
     check(hip.kvb_synchronize(), "synchronize")
 
 
+def set_stream(stream):
+    """Queues the library's work on `stream` (a hipStream_t as an int or c_void_p; None: the
+    library's own), after everything already queued on the previous stream (kvb_set_stream)."""
+    check(hip.kvb_set_stream(stream), "set_stream")
+
+
 def run_read_bandwidth(buf: Buffer) -> float:
     ms = ctypes.c_double()
     check(hip.kvb_run_read_bandwidth(buf.ptr, buf.nbytes // 16 * 16, ctypes.byref(ms)), "run_read_bandwidth")

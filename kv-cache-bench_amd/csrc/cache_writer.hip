@@ -17,7 +17,7 @@ constexpr int kWriterThreads = 256;
 
 __global__ __launch_bounds__(kWriterThreads) void scatter_kernel(CacheWriteParams p) {
     const int kvh = blockIdx.x, b = blockIdx.y, blk_i = blockIdx.z;
-    const int len = p.seq_lens[b], t0 = blk_i * p.page_size;
+    const int len = live_len(p.seq_lens, b, p.len_cap), t0 = blk_i * p.page_size;
     if (t0 >= len) return;
     const int rows = min(len - t0, p.page_size);
     const size_t row_bytes = (size_t)p.head_dim * p.elem_size;
@@ -64,7 +64,7 @@ constexpr int kQuantRegs = 16;
 
 __global__ __launch_bounds__(kWriterThreads) void quantize_kernel(CacheWriteParams p) {
     const int kvh = blockIdx.x, b = blockIdx.y, blk_i = blockIdx.z;
-    const int len = p.seq_lens[b], t0 = blk_i * p.page_size;
+    const int len = live_len(p.seq_lens, b, p.len_cap), t0 = blk_i * p.page_size;
     if (t0 >= len) return;  // uniform over the workgroup, before the barrier in block_max
     const int rows = min(len - t0, p.page_size);
     const size_t n4 = (size_t)rows * p.head_dim / 4;  // groups of 4 values (head_dim % 4 == 0)

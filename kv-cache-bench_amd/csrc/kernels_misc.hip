@@ -15,7 +15,7 @@ constexpr float kNegBigR = -1e30f;
 template <int D>
 __global__ __launch_bounds__(D) void paged_reduce_kernel(ReduceParams p) {
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x, H = p.num_heads;
-    const int parts = (p.seq_lens[b] + p.part_tokens - 1) / p.part_tokens;
+    const int parts = (live_len(p.seq_lens, b, p.len_cap) + p.part_tokens - 1) / p.part_tokens;  // <= max_parts
     float* o = p.out + ((size_t)b * H + h) * D;
     if (parts <= 0) {
         o[d] = 0.0f;
@@ -40,58 +40,98 @@ __device__ __forceinline__ float kv_at(const void* base, size_t i) {
     else return static_cast<const float*>(base)[i];
 }
 
-// One thread per (t, h, b): scores[b][h][t] = scale * q . k_t (src/kernels.metal:152-166).
-template <int KIND>
-__global__ __launch_bounds__(256) void naive_scores_kernel(NaiveParams p, int D, int G) {
-    const int t = blockIdx.x * 256 + threadIdx.x, h = blockIdx.y, b = blockIdx.z, H = p.num_heads;
-    if (t >= p.seq_lens[b]) return;
-    const size_t krow = (((size_t)b * p.num_kv_heads + h / G) * p.max_len + t) * D;
-    const float* qh = p.q + ((size_t)b * H + h) * D;
-    float s = 0.0f;
-    for (int d = 0; d < D; ++d) s += qh[d] * kv_at<KIND>(p.k, krow + d);
-    p.scores[((size_t)b * H + h) * p.max_len + t] = s * p.scale;
+// ---- naive three-pass baseline (the reference's run_naive, src/kernels.metal:149-218) ----------
+// The comparison point for paged_decode: the same attention in three launches with the scores in
+// global memory, over the contiguous cache [B][Hkv][max_len][D] (f32 or f16). The passes are laid out
+// for wave64 here: one wave per 16 tokens (scores), per row (softmax) and per row (P V).
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_max_f(float x) {
+    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+    return x;
+}
+__device__ __forceinline__ float wave_sum_f(float x) {
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
 }
 
-// One workgroup of 256 threads per (h, b): max, exp-sum, normalise in place (src/kernels.metal:168-203).
-__global__ __launch_bounds__(256) void naive_softmax_kernel(NaiveParams p) {
-    __shared__ float red[256];
-    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, len = p.seq_lens[b];
+// Pass 1, scores[b][h][t] = scale * q . k_t. Grid (ceil(max_len / 16), H, B), one wave each: the
+// lanes of quad k take token 16 x + k, lane 4k + j the j-th quarter of its row (D / 4 contiguous
+// elements in 16-byte loads, so a quad reads the whole row), and the quad's partial dot products
+// are summed by two DPP quad swaps.
+template <int KIND, int D>
+__global__ __launch_bounds__(64) void naive_scores_kernel(NaiveParams p, int G) {
+    constexpr int ESZ = KIND == KV_F16 ? 2 : 4, QD = D / 4, PER = 16 / ESZ, NL = QD / PER;
+    const int lane = threadIdx.x, h = blockIdx.y, b = blockIdx.z, H = p.num_heads;
+    const int len = live_len(p.seq_lens, b, p.max_len);
+    if ((int)blockIdx.x * 16 >= len) return;  // uniform
+    const int t = blockIdx.x * 16 + (lane >> 2), qd = lane & 3;
+    const bool live = t < len;
+    const int ts = live ? t : 0;  // lanes past the end read row 0 and write nothing
+    const float* qh = p.q + ((size_t)b * H + h) * D + qd * QD;
+    const char* krow = static_cast<const char*>(p.k) +
+                       ((((size_t)b * p.num_kv_heads + h / G) * p.max_len + ts) * D + qd * QD) * ESZ;
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const uint4 w = *reinterpret_cast<const uint4*>(krow + 16 * i);
+        if constexpr (KIND == KV_F16) {
+            const _Float16* x = reinterpret_cast<const _Float16*>(&w);
+#pragma unroll
+            for (int e = 0; e < PER; ++e) s = __builtin_fmaf(qh[i * PER + e], (float)x[e], s);
+        } else {
+            const float* x = reinterpret_cast<const float*>(&w);
+#pragma unroll
+            for (int e = 0; e < PER; ++e) s = __builtin_fmaf(qh[i * PER + e], x[e], s);
+        }
+    }
+    s += dpp_f<0xB1>(s);  // quad_perm [1,0,3,2]
+    s += dpp_f<0x4E>(s);  // quad_perm [2,3,0,1]
+    if (live && qd == 0) p.scores[((size_t)b * H + h) * p.max_len + t] = s * p.scale;
+}
+
+// Pass 2, softmax in place. Grid (H, B), one wave per row: max, exp and sum, scale, each a sweep of
+// the row 64 tokens at a time with the wave's reductions by lane shuffles.
+__global__ __launch_bounds__(64) void naive_softmax_kernel(NaiveParams p) {
+    const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+    const int len = live_len(p.seq_lens, b, p.max_len);
     float* row = p.scores + ((size_t)b * p.num_heads + h) * p.max_len;
     float mx = kNegBigR;
-    for (int t = tid; t < len; t += 256) mx = fmaxf(mx, row[t]);
-    red[tid] = mx;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
-        __syncthreads();
-    }
-    mx = red[0];
-    __syncthreads();
+    for (int t = lane; t < len; t += 64) mx = fmaxf(mx, row[t]);
+    mx = wave_max_f(mx);
     float sum = 0.0f;
-    for (int t = tid; t < len; t += 256) {
+    for (int t = lane; t < len; t += 64) {
         const float e = __expf(row[t] - mx);
         row[t] = e;
         sum += e;
     }
-    red[tid] = sum;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (tid < s) red[tid] += red[tid + s];
-        __syncthreads();
-    }
-    const float inv = 1.0f / red[0];
-    for (int t = tid; t < len; t += 256) row[t] *= inv;
+    const float inv = 1.0f / wave_sum_f(sum);
+    for (int t = lane; t < len; t += 64) row[t] *= inv;
 }
 
-// One thread per (d, h, b): out[b][h][d] = sum_t p_t v_t[d] (src/kernels.metal:205-218).
-template <int KIND>
-__global__ void naive_pv_kernel(NaiveParams p, int D, int G) {
-    const int d = threadIdx.x, h = blockIdx.x, b = blockIdx.y, H = p.num_heads, len = p.seq_lens[b];
+// Pass 3, out[b][h] = sum_t p_t v_t. Grid (H, B), one wave per row: lane l owns D / 64 adjacent
+// elements, so each token's V row is one contiguous read across the wave; p_t is the same for every
+// lane. An empty sequence writes 0.
+template <int KIND, int D>
+__global__ __launch_bounds__(64) void naive_pv_kernel(NaiveParams p, int G) {
+    constexpr int DL = D / 64;
+    const int lane = threadIdx.x, h = blockIdx.x, b = blockIdx.y, H = p.num_heads;
+    const int len = live_len(p.seq_lens, b, p.max_len);
     const float* pr = p.scores + ((size_t)b * H + h) * p.max_len;
-    const size_t vbase = ((size_t)b * p.num_kv_heads + h / G) * p.max_len * D + d;
-    float o = 0.0f;
-    for (int t = 0; t < len; ++t) o += pr[t] * kv_at<KIND>(p.v, vbase + (size_t)t * D);
-    p.out[((size_t)b * H + h) * D + d] = o;
+    const size_t vbase = ((size_t)b * p.num_kv_heads + h / G) * p.max_len * D + (size_t)lane * DL;
+    float o[DL];
+#pragma unroll
+    for (int j = 0; j < DL; ++j) o[j] = 0.0f;
+    for (int t = 0; t < len; ++t) {
+        const float pt = pr[t];
+#pragma unroll
+        for (int j = 0; j < DL; ++j) o[j] = __builtin_fmaf(pt, kv_at<KIND>(p.v, vbase + (size_t)t * D + j), o[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < DL; ++j) p.out[((size_t)b * H + h) * D + (size_t)lane * DL + j] = o[j];
 }
 
 // fp64 attention over the contiguous cache, one workgroup per (h, b): the reference's
@@ -115,7 +155,8 @@ __device__ double block_reduce_double(double x, bool is_max) {
 
 template <int KIND>
 __global__ __launch_bounds__(256) void attention_fp64_kernel(NaiveParams p, int D, int G) {
-    const int h = blockIdx.x, b = blockIdx.y, H = p.num_heads, len = p.seq_lens[b], tid = threadIdx.x;
+    const int h = blockIdx.x, b = blockIdx.y, H = p.num_heads, len = live_len(p.seq_lens, b, p.max_len);
+    const int tid = threadIdx.x;
     const size_t kv0 = ((size_t)b * p.num_kv_heads + h / G) * p.max_len * D;
     const double scale = p.scale;  // the reference's float 1/sqrt(D), widened
     __shared__ double s_q[128];
@@ -152,13 +193,13 @@ __global__ __launch_bounds__(256) void attention_fp64_kernel(NaiveParams p, int 
     }
 }
 
-// Grid-stride streaming read with 8 independent 16-byte loads in flight per lane
-// (src/kernels.metal:220-233). XOR-accumulated; the store fires only on a sentinel no real
-// buffer of the probe (all words equal) produces.
+// The streaming-read ceiling (the reference's read_bw, src/kernels.metal:220-233), one workgroup per
+// CU: workgroup g reads the contiguous words [g * per_group, (g + 1) * per_group), kReadBwThreads at
+// a time, kReadBwUnroll non-temporal 16-byte loads in flight per thread (32 KB per workgroup). The
+// words are XOR-accumulated; the store fires only on a sentinel that no buffer the probe reads (all
+// words equal) produces.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-// Workgroup g reads the contiguous words [g * per_group, (g + 1) * per_group), kReadBwThreads at a
-// time, kReadBwUnroll loads in flight per thread (32 KB per workgroup).
 __global__ __launch_bounds__(kReadBwThreads) void read_bw_kernel(const u32x4_t* __restrict__ src, size_t n16,
                                                                  size_t per_group, float* sink) {
     const size_t beg = (size_t)blockIdx.x * per_group;
@@ -196,15 +237,26 @@ hipError_t launch_paged_reduce(int head_dim, const ReduceParams& p, int batch, h
     return hipGetLastError();
 }
 
+template <int KIND, int D>
+void launch_naive_passes(const NaiveParams& p, int group, int batch, hipStream_t s, const Marks& m) {
+    const dim3 sgrid((unsigned)((p.max_len > 0 ? p.max_len : 1) + 15) / 16, p.num_heads, batch);
+    const Marks first{m.start, nullptr}, last{nullptr, m.stop};
+    launch_marked(naive_scores_kernel<KIND, D>, sgrid, dim3(64), s, first, p, group);
+    hipLaunchKernelGGL(naive_softmax_kernel, dim3(p.num_heads, batch), dim3(64), 0, s, p);
+    launch_marked(naive_pv_kernel<KIND, D>, dim3(p.num_heads, batch), dim3(64), s, last, p, group);
+}
+
 hipError_t launch_naive(int kind, int head_dim, int group, const NaiveParams& p, int batch, hipStream_t s,
                         const Marks& m) {
-    const dim3 sgrid((unsigned)((p.max_len > 0 ? p.max_len : 1) + 255) / 256, p.num_heads, batch);
-    const Marks first{m.start, nullptr}, last{nullptr, m.stop};
-    if (kind == KV_F16) launch_marked(naive_scores_kernel<KV_F16>, sgrid, dim3(256), s, first, p, head_dim, group);
-    else launch_marked(naive_scores_kernel<KV_F32>, sgrid, dim3(256), s, first, p, head_dim, group);
-    hipLaunchKernelGGL(naive_softmax_kernel, dim3(p.num_heads, batch), dim3(256), 0, s, p);
-    if (kind == KV_F16) launch_marked(naive_pv_kernel<KV_F16>, dim3(p.num_heads, batch), dim3(head_dim), s, last, p, head_dim, group);
-    else launch_marked(naive_pv_kernel<KV_F32>, dim3(p.num_heads, batch), dim3(head_dim), s, last, p, head_dim, group);
+    if (head_dim == 64) {
+        if (kind == KV_F16) launch_naive_passes<KV_F16, 64>(p, group, batch, s, m);
+        else launch_naive_passes<KV_F32, 64>(p, group, batch, s, m);
+    } else if (head_dim == 128) {
+        if (kind == KV_F16) launch_naive_passes<KV_F16, 128>(p, group, batch, s, m);
+        else launch_naive_passes<KV_F32, 128>(p, group, batch, s, m);
+    } else {
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -19,6 +19,16 @@ constexpr int decode_waves(int /*kind*/) { return 4; }
 // Tokens one wave handles per step of its loop: the N of a 16x16 MFMA tile.
 constexpr int kTile = 16;
 
+// A sequence's length as a kernel uses it: seq_lens[b] (device memory) clamped to [0, cap], where
+// cap is what the host sized the launch for (run_paged: min(max_blocks * page_size,
+// max_parts * part_tokens); the naive kernels: max_len). The host validates its own copy of the
+// lengths; if the device copy disagrees, the clamp keeps every block-table read inside the
+// sequence's row, every workspace access inside its (sequence, head) slots and every contiguous-cache
+// read inside its max_len rows. When the two copies agree, as they must, the clamp changes nothing.
+__device__ __forceinline__ int live_len(const int32_t* seq_lens, int b, int cap) {
+    return max(0, min(seq_lens[b], cap));
+}
+
 struct DecodeParams {
     const float* q;             // [B][H][D]
     const void* k;              // [blocks][Hkv][page][D]
@@ -36,6 +46,7 @@ struct DecodeParams {
     int max_blocks;
     int max_parts;
     int part_tokens;
+    int len_cap;                // live_len's cap: min(max_blocks * page_size, max_parts * part_tokens)
     float qscale;               // softmax scale * log2(e): scores are kept in base-2 units
     // Fused merge (null: leave the merge to paged_reduce). The last workgroup of a (sequence,
     // head group) to finish merges its partitions into out; counters[b * (H / qg) + group] counts
@@ -81,6 +92,7 @@ struct ReduceParams {
     int num_heads;
     int max_parts;
     int part_tokens;
+    int len_cap;                // as DecodeParams::len_cap
 };
 
 struct NaiveParams {
@@ -149,6 +161,7 @@ struct CacheWriteParams {
     int max_blocks;
     int max_len;
     int quantize;               // 1: fp32 -> int8 with per-(block, KV head) scales
+    int len_cap;                // live_len's cap: min(max_len, max_blocks * page_size)
 };
 // grid (Hkv, batch, max_blocks_used): max_blocks_used = ceil(max_len / page)
 hipError_t launch_write_paged(const CacheWriteParams& p, int batch, int max_blocks_used, hipStream_t s,

@@ -218,12 +218,17 @@ __device__ __forceinline__ int wave_inclusive_sum(int x) {
     return x;
 }
 
-__device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int batch, int part_tokens, int i) {
+// Item i of `items` (the launch's grid y, counted by the host from its copy of the lengths). If the
+// lengths in seq_lens (clamped by live_len) make a different number of items, the two copies
+// disagree: every workgroup then gets no item and the launch does nothing, rather than leave some
+// partitions unlaunched and their group's arrival counter short of its count for later launches.
+__device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int batch, int part_tokens, int len_cap,
+                                                int i, int items) {
     constexpr int E = kRaggedMaxBatch / 64;
     const int lane = threadIdx.x & 63;
     const int ne = (batch + 63) >> 6;
     int len[E];
-    for (int e = 0; e < E; ++e) len[e] = (e < ne && 64 * e + lane < batch) ? seq_lens[64 * e + lane] : 0;
+    for (int e = 0; e < E; ++e) len[e] = (e < ne && 64 * e + lane < batch) ? live_len(seq_lens, 64 * e + lane, len_cap) : 0;
     WorkItem r{-1, 0};
     // full partitions, in sequence order: an exclusive scan of len / part_tokens
     int before = 0;
@@ -238,16 +243,23 @@ __device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int bat
         }
         before += __builtin_amdgcn_readlane(s, 63);
     }
-    if (r.b < 0) {
-        // partial last partitions, longest first: the (i - full)-th largest key rem << 16 | (0xFFFF - b),
-        // found bit by bit from the top (keys are distinct; 0 marks a sequence without one)
-        int j = i - before, npart = 0;
-        unsigned key[E];
-        for (int e = 0; e < E; ++e) {
-            const int rem = len[e] % part_tokens;
-            key[e] = (e < ne && rem > 0) ? ((unsigned)rem << 16) | (0xFFFFu - (unsigned)(64 * e + lane)) : 0u;
-            if (e < ne) npart += __popcll(__ballot(key[e] != 0u));
+    // partial last partitions: keys rem << 16 | (0xFFFF - b) (distinct; 0 marks a sequence without
+    // one); then the empty sequences
+    int npart = 0, nempty = 0;
+    unsigned key[E];
+    for (int e = 0; e < E; ++e) {
+        const int rem = len[e] % part_tokens;
+        key[e] = (e < ne && rem > 0) ? ((unsigned)rem << 16) | (0xFFFFu - (unsigned)(64 * e + lane)) : 0u;
+        if (e < ne) {
+            npart += __popcll(__ballot(key[e] != 0u));
+            nempty += __popcll(__ballot(len[e] == 0 && 64 * e + lane < batch));
         }
+    }
+    if (before + npart + nempty != items) return WorkItem{-1, 0};  // uniform: the lengths disagree
+    if (r.b < 0) {
+        // partial last partitions, longest first: the (i - full)-th largest key, found bit by bit
+        // from the top
+        int j = i - before;
         if (j < npart) {
             unsigned want = 0;
             const int top = 16 + (32 - __builtin_clz((unsigned)part_tokens));  // keys < 2^top
@@ -311,13 +323,13 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // fp16: 486 -> 366 us; equal lengths under a longer max_len ran 1.7x slower).
     int part = blockIdx.z, b = blockIdx.y;
     if (p.ragged_items) {
-        const WorkItem it = ragged_item(p.seq_lens, p.batch, p.part_tokens, blockIdx.y);
+        const WorkItem it = ragged_item(p.seq_lens, p.batch, p.part_tokens, p.len_cap, blockIdx.y, gridDim.y);
         if (it.b < 0 || it.b >= p.batch || it.part >= p.max_parts) return;  // uniform, before any barrier
         b = it.b;
         part = it.part;
     }
     const int h0 = blockIdx.x * QG;
-    const int len = p.seq_lens[b];
+    const int len = live_len(p.seq_lens, b, p.len_cap);  // nparts <= max_parts, t1 <= max_blocks * P
     const int t0 = part * p.part_tokens;
     const int H = p.num_heads, Hkv = p.num_kv_heads, P = p.page_size;
     if (t0 >= len) {  // uniform over the workgroup, before any barrier
@@ -349,12 +361,15 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
             if constexpr (FAST) {
                 // [th, th+16) lies in one page: one block id and a buffer resource over exactly its
                 // live rows; a half at or past t1 (the prefetch after the last tile) gets an empty one.
+                // A block id of -1 (an unused table entry, reachable only when seq_lens disagrees with
+                // the host's lengths) reads as an empty page.
                 const int tc = min(th, t1 - 1);
-                const int blk = bt[tc / P];
+                const int braw = bt[tc / P];
+                const int blk = max(braw, 0);
                 const size_t row0 = ((size_t)blk * Hkv + kvh) * P + (tc % P);
                 // (readfirstlane between the min and the max: the value is wave-uniform, and fused
                 // into one v_med3 it would land in a VGPR the prefetch may be writing)
-                const int rows = max(0, __builtin_amdgcn_readfirstlane(min(kHalf, t1 - th)));
+                const int rows = braw < 0 ? 0 : max(0, __builtin_amdgcn_readfirstlane(min(kHalf, t1 - th)));
                 const int nbytes = rows * D * T::ESZ;
                 const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
                     const_cast<char*>(kbase + row0 * D * T::ESZ), (short)0, nbytes, 0x00020000);
@@ -372,11 +387,13 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                 }
             } else {
                 // Any page size: each lane finds the block of its own token. Lanes past t1 read the
-                // partition's first token (always live) and zero what they got.
+                // partition's first token (always live) and zero what they got; a block id of -1
+                // reads as zeros too (from block 0).
                 const int tk = th + c;
-                const bool kval = tk < t1;
-                const int tks = kval ? tk : t0;
-                const size_t krow = ((size_t)bt[tks / P] * Hkv + kvh) * P + (tks % P);
+                const int tks = tk < t1 ? tk : t0;
+                const int kid = bt[tks / P];
+                const bool kval = tk < t1 && kid >= 0;
+                const size_t krow = ((size_t)max(kid, 0) * Hkv + kvh) * P + (tks % P);
                 const char* kb = kbase + krow * D * T::ESZ;
                 for (int m = 0; m < T::KLOADS; ++m) {
                     const uint4 x = *reinterpret_cast<const uint4*>(kb + T::kdoff(m, q4) * T::ESZ);
@@ -384,9 +401,10 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                 }
                 for (int i = 0; i < NV; ++i) {
                     const int tv = th + i * (64 / VL) + lane / VL;
-                    const bool vval = tv < t1;
-                    const int tvs = vval ? tv : t0;
-                    const size_t vrow = ((size_t)bt[tvs / P] * Hkv + kvh) * P + (tvs % P);
+                    const int tvs = tv < t1 ? tv : t0;
+                    const int vid = bt[tvs / P];
+                    const bool vval = tv < t1 && vid >= 0;
+                    const size_t vrow = ((size_t)max(vid, 0) * Hkv + kvh) * P + (tvs % P);
                     const uint4 x = *reinterpret_cast<const uint4*>(vbase + vrow * D * T::ESZ + (lane % VL) * 16);
                     r.v[h][i] = vval ? x : make_uint4(0, 0, 0, 0);
                 }
@@ -394,7 +412,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                     for (int i = 0; i < 4; ++i) {  // the score-layout tokens th + 4*q4 + i of this lane
                         const int ts = th + 4 * q4 + i;
                         const int tss = ts < t1 ? ts : t0;
-                        const size_t slot = (size_t)bt[tss / P] * Hkv + kvh;
+                        const size_t slot = (size_t)max(bt[tss / P], 0) * Hkv + kvh;
                         r.ks[4 * h + i] = ksc[slot];
                         r.vs[4 * h + i] = vsc[slot];
                     }

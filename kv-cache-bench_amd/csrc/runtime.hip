@@ -42,6 +42,7 @@ struct Runtime {
     void* scores = nullptr;         // naive scores (grow-only)
     size_t scores_bytes = 0;
     void* flush_buf = nullptr;      // cache-flush source
+    hipEvent_t switch_ev = nullptr; // orders a new stream after the old one (kvb_set_stream)
     int cus = 0;                    // compute units: the read probe runs one workgroup per CU
     float* sink = nullptr;          // read-probe sink
     bool pipelined = false;
@@ -110,6 +111,15 @@ int resolve_part(const kvb_paged_args* a) {
 int max_parts_of(const kvb_paged_args* a) {
     const int part = resolve_part(a);
     return std::max(1, (int)(((long long)a->max_len + part - 1) / part));
+}
+
+// The kernels' cap on a device-side length (live_len): what the block table and the workspace of
+// this launch hold, min(max_blocks * page_size, max_parts * part_tokens). The host copy of the
+// lengths has been checked against both; the cap keeps the kernels inside the buffers if the device
+// copy disagrees.
+int len_cap_of(const kvb_paged_args* a) {
+    const long long cap = std::min((long long)a->max_blocks * a->page_size, (long long)max_parts_of(a) * resolve_part(a));
+    return (int)std::min<long long>(cap, 0x7fffffff);
 }
 
 size_t workspace_need(const kvb_paged_args* a) {
@@ -197,8 +207,10 @@ int ragged_items(const kvb_paged_args* a, int part) {
     return equal || items > 65535 ? 0 : (int)items;
 }
 
+// counters: the fused merge's arrival counters (zero, at least B * H / qg ints), or null for the
+// library's own (grown on demand).
 int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, bool fused, const StepMarks& mk,
-                  bool loads_only = false) {
+                  bool loads_only = false, int* counters = nullptr) {
     const int part = resolve_part(a);
     const int qg = query_heads_per_group(a);
     kvbk::DecodeParams p{};
@@ -218,6 +230,7 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     p.max_blocks = a->max_blocks;
     p.max_parts = max_parts_of(a);
     p.part_tokens = part;
+    p.len_cap = len_cap_of(a);
     p.qscale = (1.0f / std::sqrt((float)a->head_dim)) * 1.4426950408889634f;
     p.batch = a->batch;
     p.ragged_items = ragged_items(a, part);
@@ -226,7 +239,8 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     if (fused && qg * p.max_parts > kvbk::fused_merge_slots(a->kv_type, a->head_dim)) fused = false;
     if (fused) {
         p.out = a->out;
-        if (int st = counters_for(a, &p.counters)) return st;
+        if (counters) p.counters = counters;
+        else if (int st = counters_for(a, &p.counters)) return st;
     }
     const bool fast = a->page_size % kvbk::kTile == 0 && part % kvbk::kTile == 0;
     const kvbk::Marks dm{mk.step.start ? mk.step.start : mk.decode.start, fused ? mk.step.stop : mk.decode.stop};
@@ -239,7 +253,7 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     }
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("paged_decode launch: ") + hipGetErrorString(e));
     if (fused || loads_only) return KVB_OK;
-    kvbk::ReduceParams r{part_out, part_ml, a->seq_lens, a->out, a->num_heads, p.max_parts, part};
+    kvbk::ReduceParams r{part_out, part_ml, a->seq_lens, a->out, a->num_heads, p.max_parts, part, p.len_cap};
     e = kvbk::launch_paged_reduce(a->head_dim, r, a->batch, g.stream, rm);
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("paged_reduce launch: ") + hipGetErrorString(e));
     return KVB_OK;
@@ -283,9 +297,17 @@ int kvb_device_name(char* buf, size_t cap) {
 
 const char* kvb_last_error(void) { return g_err.c_str(); }
 
+// Work already queued on the old stream uses the library's workspace and fused-merge counters, which
+// every stream shares: the new stream waits for it (an event recorded on the old stream) before any
+// work queued on it afterwards, so two steps never run at once.
 int kvb_set_stream(void* stream) {
     if (int st = ensure_device()) return st;
-    g.stream = stream ? static_cast<hipStream_t>(stream) : g.own;
+    hipStream_t next = stream ? static_cast<hipStream_t>(stream) : g.own;
+    if (next == g.stream) return KVB_OK;
+    if (!g.switch_ev) KVB_HIP(hipEventCreateWithFlags(&g.switch_ev, hipEventDisableTiming));
+    KVB_HIP(hipEventRecord(g.switch_ev, g.stream));
+    KVB_HIP(hipStreamWaitEvent(next, g.switch_ev, 0));
+    g.stream = next;
     return KVB_OK;
 }
 
@@ -461,6 +483,7 @@ int kvb_write_paged(const kvb_cache_args* a, double* ms) {
     p.max_blocks = a->max_blocks;
     p.max_len = a->max_len;
     p.quantize = a->kv_type == KVB_KV_I8;
+    p.len_cap = (int)std::min((long long)a->max_len, (long long)a->max_blocks * a->page_size);
     hipEvent_t e0, e1;
     if (int st = get_event(&e0)) return st;
     if (int st = get_event(&e1)) return st;
@@ -476,6 +499,8 @@ int kvb_check_naive(const kvb_naive_args* a) {
     if (a->kv_type != KVB_KV_F32 && a->kv_type != KVB_KV_F16) return fail(KVB_EINVAL, "unknown kv_type");
     if (int st = check_shape(a->batch, a->num_heads, a->num_kv_heads, a->head_dim)) return st;
     if (a->max_len < 0) return fail(KVB_EINVAL, "max_len < 0");
+    // launch grids (max_len / 16, H, batch) and (H, batch): y and z are at most 65535
+    if (a->batch > 65535 || a->num_heads > 65535) return fail(KVB_EINVAL, "batch or num_heads > 65535");
     if (a->batch > 0 && !a->host_seq_lens) return fail(KVB_EINVAL, "host_seq_lens is required");
     if (int st = check_lens(a->batch, a->host_seq_lens, a->max_len, (size_t)a->max_len)) return st;
     if (a->batch > 0 && (!a->q || !a->seq_lens || !a->out || (a->max_len > 0 && (!a->k || !a->v))))

@@ -405,7 +405,17 @@ typedef struct {
     int part_tokens, max_parts, waves;
     float *ws_out, *ws_ml, *out; /* workspace [B*H*max_parts + 1 spare][D] and [..][2], NaN-filled */
     int phase, worker, threads;
+    int len_cap;     /* the kernel's live_len cap: min(max_blocks * page_size, max_parts * part_tokens) */
+    int* violations; /* accesses that would leave the sequence's table row or its workspace slots */
 } split_job;
+
+/* The kernel's live_len: a length from `lens` (the device copy) clamped to [0, len_cap]. */
+static int model_len(const split_job* j, int b) {
+    const int len = j->lens[b];
+    return len < 0 ? 0 : len > j->len_cap ? j->len_cap : len;
+}
+
+static void model_violation(const split_job* j) { __atomic_fetch_add(j->violations, 1, __ATOMIC_RELAXED); }
 
 static void load_row(const void* pool, int kv_type, size_t at, int D, float* dst) {
     for (int d = 0; d < D; ++d) {
@@ -420,7 +430,7 @@ static void model_partition(const split_job* j, int b, int h, int part) {
     const kvbo_shape* s = j->s;
     const int D = s->head_dim, P = j->page_size, Hkv = s->num_kv_heads;
     const int kvh = h / (s->num_heads / Hkv);
-    const int len = j->lens[b];
+    const int len = model_len(j, b);
     const int t0 = part * j->part_tokens;
     if (t0 >= len) return; /* an empty partition writes nothing */
     const int t1 = len < t0 + j->part_tokens ? len : t0 + j->part_tokens;
@@ -437,10 +447,16 @@ static void model_partition(const split_job* j, int b, int h, int part) {
             float mt = -INFINITY;
             for (int i = 0; i < n; ++i) {
                 const int t = tt + i;
-                const size_t blk = (size_t)bt[t / P];
+                if (t / P >= j->max_blocks) model_violation(j); /* the clamp keeps t < max_blocks * P */
+                const int32_t id = t / P < j->max_blocks ? bt[t / P] : 0;
+                /* a block id of -1 (an unused entry: seq_lens disagrees with the host) reads as
+                   zeros, with block 0's scales, as in the kernel */
+                const size_t blk = id < 0 ? 0 : (size_t)id;
                 const size_t row = ((blk * Hkv + kvh) * P + t % P) * D;
                 load_row(j->k, j->kv_type, row, D, krow);
                 load_row(j->v, j->kv_type, row, D, vrow[i]);
+                if (id < 0)
+                    for (int d = 0; d < D; ++d) krow[d] = vrow[i][d] = 0.0f;
                 float dot = 0.0f;
                 for (int d = 0; d < D; ++d) dot += qr[d] * krow[d];
                 sc[i] = dot * j->scale;
@@ -489,7 +505,11 @@ static void model_reduce(const split_job* j, int b, int h) {
     const int D = j->s->head_dim;
     const size_t row = (size_t)b * j->s->num_heads + h;
     float* out = j->out + row * D;
-    const int parts = (j->lens[b] + j->part_tokens - 1) / j->part_tokens;
+    int parts = (model_len(j, b) + j->part_tokens - 1) / j->part_tokens;
+    if (parts > j->max_parts) { /* the clamp keeps parts <= max_parts */
+        model_violation(j);
+        parts = j->max_parts;
+    }
     if (parts == 0) { /* an empty sequence attends to nothing */
         for (int d = 0; d < D; ++d) out[d] = 0.0f;
         return;
@@ -546,11 +566,15 @@ int kvbo_split_decode(const kvbo_shape* s, int kv_type, int page_size, int max_b
     if (threads < 1) threads = 1;
     if (rows > 0 && threads > rows) threads = rows;
     split_job* jobs = (split_job*)malloc(sizeof(split_job) * (size_t)threads);
+    const long long cap_table = (long long)max_blocks * page_size, cap_ws = (long long)max_parts * part_tokens;
+    const int len_cap = (int)(cap_table < cap_ws ? cap_table : cap_ws);
+    int violations = 0;
     pthread_t* tids = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
     for (int phase = 0; phase < 2 && rows > 0; ++phase) { /* decode, then merge: two kernels */
         for (int w = 0; w < threads; ++w) {
             split_job j = {s, kv_type, page_size, max_blocks, table, lens, q, k_scale, v_scale, k_pool, v_pool,
-                           scale, part_tokens, max_parts, waves, ws_out, ws_ml, out, phase, w, threads};
+                           scale, part_tokens, max_parts, waves, ws_out, ws_ml, out, phase, w, threads,
+                           len_cap, &violations};
             jobs[w] = j;
         }
         int started = 0;
@@ -567,5 +591,5 @@ int kvbo_split_decode(const kvbo_shape* s, int kv_type, int page_size, int max_b
     free(tids);
     free(ws_out);
     free(ws_ml);
-    return max_parts;
+    return violations ? -2 : max_parts;
 }

@@ -134,7 +134,11 @@ int kvbo_auto_part_tokens(int batch, int num_kv_heads, int max_len);
  * kv_type: 0 fp32, 1 fp16 (bit patterns), 2 int8 with k_scale / v_scale [pool blocks][Hkv].
  * part_tokens 0 means kvbo_auto_part_tokens. part_out [B][H][max_parts][D] and
  * part_ml [B][H][max_parts][2] may be NULL; the slots of empty partitions are left NaN.
- * Returns max_parts, or -1 on bad arguments.
+ * `lens` plays the kernel's device copy of the lengths and max_len the host's: as in the kernel,
+ * each length is clamped to [0, min(max_blocks * page_size, max_parts * part_tokens)] and a block id
+ * of -1 reads as zeros, so lengths that disagree with max_len and the table stay inside them.
+ * Returns max_parts; -2 if an access left a sequence's table row or its workspace slots (the
+ * model counts them); -1 on bad arguments.
  * It is the host of the mutation harness's planted kernel mistakes (tests/mutation/mutate.py), and
  * it is pinned by the same parity battery as the GPU kernels (tests/test_split_model.py). */
 int kvbo_split_decode(const kvbo_shape* s, int kv_type, int page_size, int max_blocks, const int32_t* table,

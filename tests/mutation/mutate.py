@@ -18,7 +18,8 @@ Groups:
   host    the boundary mistakes of the C ABI and the C++ host layer (scripts/mutation.sh:37-41 and
           their neighbours), planted in copies of kv-cache-bench_amd/ and include/, rebuilt with the
           package Makefile (hipcc for runtime.hip), checked by tests/test_host.py, tests/test_abi.py
-          and the C++ test programs (tests/test_cpp_programs.py, CPU part).
+          and the reference's own C++ test programs compiled against the mutated headers and
+          libraries (tests/test_cpp_programs.py, CPU part).
 
 Usage:
   python tests/mutation/mutate.py [GROUP ...] [--only SUBSTR] [--out FILE] [--keep]
@@ -39,6 +40,7 @@ import time
 from dataclasses import dataclass
 
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+REFERENCE = "/root/reference"  # the reference's test programs are rebuilt from its sources there
 ORACLE_C = "oracle/kvb_oracle.c"
 RUNTIME = "kv-cache-bench_amd/csrc/runtime.hip"
 GROUP_TESTS = {
@@ -84,7 +86,8 @@ MUTANTS = [
     K("partition merge drops the last partition",
       "for (int i = 0; i < parts; ++i) {", "for (int i = 0; i < parts - 1; ++i) {"),
     K("block table ignored (logical = physical)",
-      "const size_t blk = (size_t)bt[t / P];", "const size_t blk = (size_t)(t / P);"),
+      "const int32_t id = t / P < j->max_blocks ? bt[t / P] : 0;",
+      "const int32_t id = t / P < j->max_blocks ? (int32_t)(t / P) : 0;"),
     K("int8: K scale not applied", "sc[i] *= j->k_scale[blk * Hkv + kvh];", ";"),
     K("int8: K scale of KV head 0 for every head",
       "sc[i] *= j->k_scale[blk * Hkv + kvh];", "sc[i] *= j->k_scale[blk * Hkv];"),
@@ -94,8 +97,8 @@ MUTANTS = [
       "vs[i] = j->v_scale[blk * Hkv + kvh];", "vs[i] = j->v_scale[(size_t)bt[0] * Hkv + kvh];"),
     K("partition merge never writes the output", "out[d] = o / L;", "(void)o;"),
     K("partition merge takes one partition too many at an exact multiple",
-      "const int parts = (j->lens[b] + j->part_tokens - 1) / j->part_tokens;",
-      "const int parts = j->lens[b] / j->part_tokens + 1;"),
+      "int parts = (model_len(j, b) + j->part_tokens - 1) / j->part_tokens;",
+      "int parts = model_len(j, b) / j->part_tokens + 1;"),
     K("partition merge has no case for an empty sequence", "if (parts == 0) {", "if (0) {"),
     K("query head served by the wrong KV head",
       "const int kvh = h / (s->num_heads / Hkv);", "const int kvh = h % Hkv;"),
@@ -107,6 +110,8 @@ MUTANTS = [
       "tt += j->waves * kModelTile", "tt += 2 * j->waves * kModelTile"),
     K("wave merge weight exp(M - m) instead of exp(m - M)",
       "wt[w] = exp_ftz(wm[w] - M);", "wt[w] = exp_ftz(M - wm[w]);"),
+    K("device length not clamped to what the launch holds",
+      "return len < 0 ? 0 : len > j->len_cap ? j->len_cap : len;", "return len;"),
     K("partition weight without l (w = exp(m - M))",
       "const float w = ml[2 * i + 1] * exp_ftz(ml[2 * i] - M);", "const float w = exp_ftz(ml[2 * i] - M);"),
     # ---- the checker ----
@@ -235,12 +240,16 @@ def prepare(m: Mutant, work: str) -> tuple[dict, str]:
         env["KVBO_LIB"] = os.path.join(work, "oracle", "build", "libkvb_oracle.so")
     else:
         skip = shutil.ignore_patterns("__pycache__")
-        for d in ("kv-cache-bench_amd", "include", "tests/cpp"):
+        for d in ("kv-cache-bench_amd", "include"):
             _copy(d, work, skip)
-        for f in ("oracle/kvb_oracle.h", "oracle/build/libkvb_oracle.so"):
+        for f in ("oracle/Makefile", "oracle/kvref.map", "oracle/kvb_oracle.h", "oracle/build/libkvb_oracle.so",
+                  "oracle/_ref/libkvref.so"):
             _copy(f, work)
-        cmd = ["make", "-C", os.path.join(work, "kv-cache-bench_amd"), "-j8"]
-        env["KVB_BUILD_DIR"] = os.path.join(work, "kv-cache-bench_amd", "build")
+        # the package, then the reference's test programs against the mutated headers and libraries
+        pkg = os.path.join(work, "kv-cache-bench_amd")
+        cmd = ["bash", "-c", f"make -C {pkg} -j8 && make -C {os.path.join(work, 'oracle')} ref-tests REF={REFERENCE}"]
+        env["KVB_BUILD_DIR"] = os.path.join(pkg, "build")
+        env["KVB_REF_BIN"] = os.path.join(work, "oracle", "_ref")
     path = os.path.join(work, m.path)
     with open(path) as f:
         text = mutated_text(m, f.read())

@@ -197,6 +197,45 @@ def test_steps_pipelined_and_deterministic(gpu):
     dev.free()
 
 
+def test_stream_switch_orders_queued_steps(gpu):
+    """kvb_set_stream while steps are still queued on the previous stream. Every stream shares the
+    library's split-K workspace and fused-merge counters, so the new stream must wait for the old
+    one. Two cases queued on alternating streams in pipelined mode (nothing waits in between) give
+    the bits each gives alone, three times over."""
+    import ctypes
+    kvb = gpu
+    hiprt = ctypes.CDLL("libamdhip64.so")  # the HIP runtime libkvb_hip already loaded
+    streams = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for s in streams:
+        assert hiprt.hipStreamCreate(ctypes.byref(s)) == 0
+    cases = []
+    for i, lens in enumerate(([16384, 16384], [9000, 3000, 12000])):
+        w = kvb.Workload(kvb.Shape(len(lens), 32, 8, 128), "f16", lens, seed=80 + i)
+        dev = kvb.DeviceCase(w, kvb.PagedCache(w, 16, 7 + i, pool_factor=1.5))
+        dev.run(1024)
+        cases.append((dev, dev.output()))
+    try:
+        for rep in range(3):
+            progress(f"[parity] stream switch, round {rep}")
+            for dev, _ in cases:
+                dev.out.fill(0xFF)
+            kvb.begin_pipelined()
+            for i in range(4):
+                kvb.set_stream(streams[i % 2])
+                cases[i % 2][0].run(1024)
+            kvb.set_stream(None)
+            assert len(kvb.end_pipelined()) == 4
+            for dev, want in cases:
+                assert np.array_equal(dev.output(), want)
+    finally:
+        kvb.set_stream(None)
+        kvb.synchronize()
+        for s in streams:
+            hiprt.hipStreamDestroy(s)
+        for dev, _ in cases:
+            dev.free()
+
+
 @pytest.mark.parametrize("kv", ["f32", "f16", "i8"])
 def test_loads_only_decode(gpu, kv):
     """kvb_run_paged_loads (the decode's loads, no arithmetic) runs on equal and ragged lengths,

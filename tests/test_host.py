@@ -201,3 +201,16 @@ class TestRefusals:
         assert kvb.hip.kvb_paged_workspace_bytes(ctypes.byref(a)) == 16 * (128 * 4 + 8)
         a.part_tokens = 5
         assert kvb.hip.kvb_paged_max_parts(ctypes.byref(a)) == 7
+
+
+def test_c_abi_auto_part_tokens_thresholds(kvb, oracle):
+    """kvb_auto_part_tokens (the C ABI's) on the threshold table of the reference's
+    tests/boundary_tests.cpp:86-92 (16 (sequence, KV head) pairs: thresholds at 32 partitions), and
+    equal to the oracle's over a sweep of shapes and lengths."""
+    for length, part in [(0, 64), (1, 64), (3968, 64), (3969, 128), (7936, 128), (7937, 256), (15872, 256),
+                         (15873, 512), (1 << 20, 512)]:
+        assert kvb.auto_part_tokens(2, 8, length) == part
+    for b in (1, 2, 3, 16):
+        for hkv in (1, 2, 8):
+            for L in list(range(0, 5000, 37)) + [32768, 100000]:
+                assert kvb.auto_part_tokens(b, hkv, L) == oracle.auto_part_tokens(b, hkv, L)

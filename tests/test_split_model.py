@@ -77,3 +77,29 @@ def test_model_refuses_bad_arguments(kvb, oracle):
         oracle.split_decode(w.shape, 16, qc.table, w.lens, w.max_len, w.q, qc.k, qc.v)
     out, part_out, part_ml = oracle.split_decode(w.shape, 16, c.table, w.lens, w.max_len, w.q, c.k, c.v)
     assert part_out.shape == (1, 4, 1, 64) and np.isfinite(out).all()
+
+
+@pytest.mark.parametrize("kv", ["f32", "f16", "i8"])
+def test_device_lengths_that_disagree_stay_in_bounds(kvb, oracle, kv):
+    """The kernels' length clamp (live_len), on the CPU model. The host sized the launch for lengths
+    [40, 17] (max_len 40, part 16: 3 partitions; page 16: table rows of 3 blocks, capacity 48); the
+    device copy of the lengths says otherwise. The model counts every table read outside a sequence's
+    row and every merge past its partitions, and refuses (-2, a ValueError here) if there is one: so
+    returning at all shows the clamp keeps them in. A negative length gives exactly 0; a length past
+    the cap computes as the cap, with the row's unused (-1) entries read as zeros."""
+    shape = kvb.Shape(2, 8, 2, 64)
+    w = kvb.Workload(shape, kv, [40, 17], seed=3, q_amp=2.0, varied=(kv == "i8"))
+    c = kvb.PagedCache(w, 16, 5, pool_factor=1.5, poison=False)
+
+    def decode(dev_lens):
+        return oracle.split_decode(shape, 16, c.table, np.array(dev_lens, np.int32), 40, w.q, c.k, c.v,
+                                   c.k_scale, c.v_scale, part_tokens=16, threads=2)
+
+    out, _, _ = decode([-5, 1000])
+    assert (out[0] == 0).all()
+    capped, _, _ = decode([48, 48])  # the cap itself: every table entry of both rows
+    assert np.isfinite(capped).all()
+    np.testing.assert_array_equal(out[1], capped[1])
+    np.testing.assert_array_equal(decode([1000, 48])[0], capped)
+    # agreeing lengths are untouched by the clamp: the same as the host's own lengths
+    np.testing.assert_array_equal(decode([40, 17])[0], decode(w.lens)[0])
