@@ -114,6 +114,22 @@ int kvb_check_paged(const kvb_paged_args* a);
  * page_size <= 0, I8 without scales, a length < 0 or > max_len or > max_blocks * page_size,
  * head_dim not 64/128, H % Hkv != 0 (src/metal_attn.mm:72-73, 107-117, 199-201). */
 int kvb_run_paged(const kvb_paged_args* a, double* ms);
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). kvb_run_paged's decode step,
+ * with the same arguments, refusals, kernels and output bits, but the split-K workspace and the
+ * fused-merge counters live in a static device array of the library (KVB_NOALLOC_WORKSPACE_BYTES of
+ * workspace plus KVB_NOALLOC_MAX_GROUPS counters, held by every GPU the library runs on until the
+ * process ends). It allocates nothing, records no events and does not wait: the step is queued on
+ * the library's current stream (kvb_set_stream); read `out` after kvb_synchronize or the caller's
+ * own ordering. KVB_EINVAL (before any GPU work) for a->workspace set, a workspace need
+ * (kvb_paged_workspace_bytes) above KVB_NOALLOC_WORKSPACE_BYTES, batch * num_heads above
+ * KVB_NOALLOC_MAX_GROUPS, or a current device other than the library's. The library's set-up, on
+ * its first call of any entry point, resolves the array's address and zeroes its counters (which
+ * every step leaves at 0): make that first call outside graph capture. Every call on one GPU shares
+ * the one array: calls that overlap on a GPU (on streams not ordered with each other) race. */
+#define KVB_NOALLOC_WORKSPACE_BYTES (16u << 20)
+#define KVB_NOALLOC_MAX_GROUPS 16384
+int kvb_run_paged_noalloc(const kvb_paged_args* a);
 /* `steps` decode steps on the same inputs, back to back on one stream, one event pair around them
  * (run_paged_steps, src/metal_attn.hpp:91). */
 int kvb_run_paged_steps(const kvb_paged_args* a, int steps, double* ms);

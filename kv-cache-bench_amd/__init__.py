@@ -90,6 +90,7 @@ _SIGS = {
     "kvb_run_paged_steps": ([_PA, _i, _d], _i),
     "kvb_run_paged_split": ([_PA, _d, _d], _i),
     "kvb_run_paged_loads": ([_PA, _d], _i),
+    "kvb_run_paged_noalloc": ([_PA], _i),
     "kvb_run_naive": ([_NA, _d], _i),
     "kvb_check_naive": ([_NA], _i),
     "kvb_run_attention_fp64": ([_NA, _d], _i),

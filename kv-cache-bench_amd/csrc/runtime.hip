@@ -54,6 +54,47 @@ Runtime g;
 constexpr size_t kFlushBytes = size_t(1) << 30;
 constexpr size_t kSinkFloats = kvbk::kReadBwSink;
 
+// ---- the static scratch of kvb_run_paged_noalloc -----------------------------------------------
+// The fused-merge arrival counters (KVB_NOALLOC_MAX_GROUPS ints), then the split-K workspace
+// (KVB_NOALLOC_WORKSPACE_BYTES). Every GPU the library runs on holds one copy until the process
+// ends. In host code `scratch` is only a handle for hipGetSymbolAddress: the device address is
+// g.scratch_dev, resolved once per device at set-up (ensure_device), and is what kernels are given.
+constexpr size_t kScratchCounterBytes = size_t(KVB_NOALLOC_MAX_GROUPS) * sizeof(int);
+constexpr size_t kScratchBytes = kScratchCounterBytes + KVB_NOALLOC_WORKSPACE_BYTES;
+static_assert(kScratchCounterBytes % 256 == 0, "the workspace starts 256-byte aligned");
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+struct ScratchOf {
+    int device;
+    void* dev;  // the device address of `scratch` on `device`
+};
+std::vector<ScratchOf> g_scratch;
+std::string g_scratch_err;  // why the set-up could not resolve it (reported by kvb_run_paged_noalloc)
+
+// Resolves `scratch` on the current device (once per device) and zeroes its counters, which every
+// fused launch then leaves at 0 again. Runs at set-up, outside any caller's work: the fill and the
+// wait are on the library's own stream. Returns the reason for a failure ("" on success).
+std::string resolve_scratch(int device) {
+    for (const ScratchOf& s : g_scratch)
+        if (s.device == device) return "";
+    void* ptr = nullptr;
+    if (hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)); e != hipSuccess)
+        return std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+    if (!ptr) return "hipGetSymbolAddress(scratch) returned a null address";
+    if (hipError_t e = kvbk::launch_fill(ptr, kScratchCounterBytes / 16, 0u, g.own); e != hipSuccess)
+        return std::string("scratch counter fill: ") + hipGetErrorString(e);
+    if (hipError_t e = hipStreamSynchronize(g.own); e != hipSuccess)
+        return std::string("scratch counter fill: ") + hipGetErrorString(e);
+    g_scratch.push_back({device, ptr});
+    return "";
+}
+
+void* scratch_of(int device) {
+    for (const ScratchOf& s : g_scratch)
+        if (s.device == device) return s.dev;
+    return nullptr;
+}
+
 int ensure_device() {
     if (g.ready) return KVB_OK;
     int n = 0;
@@ -62,6 +103,8 @@ int ensure_device() {
     KVB_HIP(hipDeviceGetAttribute(&g.cus, hipDeviceAttributeMultiprocessorCount, g.device));
     KVB_HIP(hipStreamCreateWithFlags(&g.own, hipStreamNonBlocking));
     if (!g.stream) g.stream = g.own;
+    // (a failure here concerns kvb_run_paged_noalloc alone, which reports it)
+    g_scratch_err = resolve_scratch(g.device);
     g.ready = true;
     return KVB_OK;
 }
@@ -401,6 +444,35 @@ int kvb_run_paged_steps(const kvb_paged_args* a, int steps, double* ms) {
 }
 
 int kvb_run_paged(const kvb_paged_args* a, double* ms) { return kvb_run_paged_steps(a, 1, ms); }
+
+// kvb_run_paged's step with the workspace and counters in `scratch` (no allocation, no events, no
+// wait). The fused merge needs B * H / qg counters, qg the query heads per workgroup, at most B * H.
+int kvb_run_paged_noalloc(const kvb_paged_args* a) {
+    if (int st = validate_paged(a)) return st;
+    if (a->workspace) return fail(KVB_EINVAL, "kvb_run_paged_noalloc takes no workspace: it uses its static scratch");
+    if (workspace_need(a) > KVB_NOALLOC_WORKSPACE_BYTES)
+        return fail(KVB_EINVAL, "kvb_run_paged_noalloc: the split-K workspace needs " + std::to_string(workspace_need(a)) +
+                                    " bytes, more than its scratch holds (KVB_NOALLOC_WORKSPACE_BYTES = " +
+                                    std::to_string((size_t)KVB_NOALLOC_WORKSPACE_BYTES) + "); use larger partitions");
+    if ((size_t)a->batch * a->num_heads > KVB_NOALLOC_MAX_GROUPS)
+        return fail(KVB_EINVAL, "kvb_run_paged_noalloc: batch * num_heads = " +
+                                    std::to_string((size_t)a->batch * a->num_heads) +
+                                    " is more than its scratch counters (KVB_NOALLOC_MAX_GROUPS = " +
+                                    std::to_string(KVB_NOALLOC_MAX_GROUPS) + ")");
+    if (int st = ensure_device()) return st;
+    int device = -1;
+    KVB_HIP(hipGetDevice(&device));
+    if (device != g.device)
+        return fail(KVB_EINVAL, "kvb_run_paged_noalloc: the library runs on device " + std::to_string(g.device) +
+                                    ", the current device is " + std::to_string(device));
+    if (a->batch == 0) return KVB_OK;
+    char* base = static_cast<char*>(scratch_of(device));
+    if (!base) return fail(KVB_ERUNTIME, "kvb_run_paged_noalloc: no scratch on this device: " + g_scratch_err);
+    const size_t slots = (size_t)a->batch * a->num_heads * (size_t)max_parts_of(a);
+    float* part_out = reinterpret_cast<float*>(base + kScratchCounterBytes);
+    float2* part_ml = reinterpret_cast<float2*>(base + kScratchCounterBytes + slots * (size_t)a->head_dim * sizeof(float));
+    return enqueue_paged(a, part_out, part_ml, true, StepMarks{}, false, reinterpret_cast<int*>(base));
+}
 
 int kvb_run_paged_split(const kvb_paged_args* a, double* decode_ms, double* reduce_ms) {
     if (decode_ms) *decode_ms = 0.0;
