@@ -29,6 +29,27 @@ __device__ __forceinline__ int live_len(const int32_t* seq_lens, int b, int cap)
     return max(0, min(seq_lens[b], cap));
 }
 
+// Division by a launch-constant divisor d >= 1 without a divide: for 0 <= n < 2^31,
+// n / d = mulhi(n, mul) >> shift with l = ceil(log2 d), mul = ceil(2^(31 + l) / d), shift = l - 1
+// (mul < 2^32 because d > 2^(l-1)); d = 1 is mul = 0 (n itself). The error of the rounded-up mul
+// adds less than n / 2^(31 + l) < 1 / d to n / d, which leaves its floor unchanged. (Checked
+// exhaustively for every n on d = 1, 3, 7, 16, 48, 64, 96, 128, 4095.)
+struct FastDiv {
+    uint32_t mul = 0, shift = 0;
+};
+inline FastDiv make_fast_div(uint32_t d) {
+    FastDiv f;
+    if (d <= 1) return f;
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    f.mul = (uint32_t)(((1ull << (31 + l)) + d - 1) / d);
+    f.shift = l - 1;
+    return f;
+}
+__device__ __forceinline__ int fast_div(int n, FastDiv f) {
+    return f.mul ? (int)(__umulhi((uint32_t)n, f.mul) >> f.shift) : n;
+}
+
 struct DecodeParams {
     const float* q;             // [B][H][D]
     const void* k;              // [blocks][Hkv][page][D]
@@ -43,6 +64,8 @@ struct DecodeParams {
     int num_kv_heads;
     int group;                  // H / Hkv
     int page_size;
+    FastDiv page_div;           // division by page_size
+    int tile_in_page;           // page_size and part_tokens are multiples of 32: a 32-token tile lies in one page
     int max_blocks;
     int max_parts;
     int part_tokens;

@@ -356,17 +356,26 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
 
     // ---- tile loads (no branches around them, so the compiler can keep a tile in flight)
     auto load_tile = [&](R& r, int tt) {
+        int braw = 0, off = 0;  // FAST: the block id of the half tile and its first row in the page
         for (int h = 0; h < 2; ++h) {
             const int th = tt + h * kHalf;  // first token of this half tile
             if constexpr (FAST) {
                 // [th, th+16) lies in one page: one block id and a buffer resource over exactly its
                 // live rows; a half at or past t1 (the prefetch after the last tile) gets an empty one.
+                // With tile_in_page the whole 32-token tile lies in one page (its first token is a
+                // multiple of 32), so the second half takes the first half's block, 16 rows further.
                 // A block id of -1 (an unused table entry, reachable only when seq_lens disagrees with
                 // the host's lengths) reads as an empty page.
                 const int tc = min(th, t1 - 1);
-                const int braw = bt[tc / P];
+                if (h == 0 || !p.tile_in_page) {
+                    const int bi = fast_div(tc, p.page_div);
+                    braw = bt[bi];
+                    off = tc - bi * P;
+                } else {
+                    off += kHalf;
+                }
                 const int blk = max(braw, 0);
-                const size_t row0 = ((size_t)blk * Hkv + kvh) * P + (tc % P);
+                const size_t row0 = ((size_t)blk * Hkv + kvh) * P + off;
                 // (readfirstlane between the min and the max: the value is wave-uniform, and fused
                 // into one v_med3 it would land in a VGPR the prefetch may be writing)
                 const int rows = braw < 0 ? 0 : max(0, __builtin_amdgcn_readfirstlane(min(kHalf, t1 - th)));
@@ -382,8 +391,13 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                     r.v[h][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
                                                               rv, (i * (64 / VL) + lane / VL) * D * T::ESZ + (lane % VL) * 16, 0, kNonTemporal));
                 if constexpr (KIND == KV_I8) {
-                    r.ks[h] = ksc[(size_t)blk * Hkv + kvh];
-                    r.vs[h] = vsc[(size_t)blk * Hkv + kvh];
+                    if (h == 0 || !p.tile_in_page) {
+                        r.ks[h] = ksc[(size_t)blk * Hkv + kvh];
+                        r.vs[h] = vsc[(size_t)blk * Hkv + kvh];
+                    } else {
+                        r.ks[h] = r.ks[0];
+                        r.vs[h] = r.vs[0];
+                    }
                 }
             } else {
                 // Any page size: each lane finds the block of its own token. Lanes past t1 read the
@@ -391,9 +405,10 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                 // reads as zeros too (from block 0).
                 const int tk = th + c;
                 const int tks = tk < t1 ? tk : t0;
-                const int kid = bt[tks / P];
+                const int kbi = fast_div(tks, p.page_div);
+                const int kid = bt[kbi];
                 const bool kval = tk < t1 && kid >= 0;
-                const size_t krow = ((size_t)max(kid, 0) * Hkv + kvh) * P + (tks % P);
+                const size_t krow = ((size_t)max(kid, 0) * Hkv + kvh) * P + (tks - kbi * P);
                 const char* kb = kbase + krow * D * T::ESZ;
                 for (int m = 0; m < T::KLOADS; ++m) {
                     const uint4 x = *reinterpret_cast<const uint4*>(kb + T::kdoff(m, q4) * T::ESZ);
@@ -402,9 +417,10 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                 for (int i = 0; i < NV; ++i) {
                     const int tv = th + i * (64 / VL) + lane / VL;
                     const int tvs = tv < t1 ? tv : t0;
-                    const int vid = bt[tvs / P];
+                    const int vbi = fast_div(tvs, p.page_div);
+                    const int vid = bt[vbi];
                     const bool vval = tv < t1 && vid >= 0;
-                    const size_t vrow = ((size_t)max(vid, 0) * Hkv + kvh) * P + (tvs % P);
+                    const size_t vrow = ((size_t)max(vid, 0) * Hkv + kvh) * P + (tvs - vbi * P);
                     const uint4 x = *reinterpret_cast<const uint4*>(vbase + vrow * D * T::ESZ + (lane % VL) * 16);
                     r.v[h][i] = vval ? x : make_uint4(0, 0, 0, 0);
                 }
@@ -412,7 +428,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                     for (int i = 0; i < 4; ++i) {  // the score-layout tokens th + 4*q4 + i of this lane
                         const int ts = th + 4 * q4 + i;
                         const int tss = ts < t1 ? ts : t0;
-                        const size_t slot = (size_t)max(bt[tss / P], 0) * Hkv + kvh;
+                        const size_t slot = (size_t)max(bt[fast_div(tss, p.page_div)], 0) * Hkv + kvh;
                         r.ks[4 * h + i] = ksc[slot];
                         r.vs[4 * h + i] = vsc[slot];
                     }

@@ -270,6 +270,8 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     p.num_kv_heads = a->num_kv_heads;
     p.group = a->num_heads / a->num_kv_heads;
     p.page_size = a->page_size;
+    p.page_div = kvbk::make_fast_div((uint32_t)a->page_size);
+    p.tile_in_page = a->page_size % 32 == 0 && part % 32 == 0;
     p.max_blocks = a->max_blocks;
     p.max_parts = max_parts_of(a);
     p.part_tokens = part;
