@@ -72,6 +72,36 @@ def warm_chain(kvb, dev, part, steps=20):
     return dev.run(part, steps=steps) / steps
 
 
+def warm_steps(kvb, dev, part, steps=30):
+    """Single steps with no flush between them (one launch and event pair each, waited for): beside
+    the cold steps, what the flush changes."""
+    dev.run(part)
+    return statistics.median(dev.run(part) for _ in range(steps))
+
+
+def empty_steps(kvb, w, part, steps=30):
+    """The same launch (shape, partition, grid of one partition per head group) with every sequence
+    empty: each workgroup writes its zero output and exits. The floor that dispatch and the event pair
+    put under any step of this shape."""
+    we = kvb.Workload(w.shape, w.kv_type, [0] * w.shape.batch, seed=1)
+    de = kvb.DeviceCase(we, kvb.PagedCache(we, 16, 1, poison=False))
+    de.run(part)
+    t = statistics.median(de.run(part) for _ in range(steps))
+    de.free()
+    return t
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: the CPUs this process may run on (the counterpart of the
+    reference's std::thread::hardware_concurrency, bench/bench.cpp:94), at most 16, the CPU share of
+    one GPU on the machines this runs on."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
 def cpu_model():
     """The host CPU's model name (/proc/cpuinfo), and the core count the OS reports."""
     try:
@@ -88,7 +118,7 @@ def cpu_baseline(kvb, oracle, w, c, seconds_budget=20.0, max_bytes=1 << 30):
     on the longest prefix of sequences that fits (at least one non-empty one): all heads, full
     context. int8 caches are dequantised first (outside the timing), as the reference's
     PagedCache::reference does."""
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = cpu_threads()
     esz = {kvb.KV_F32: 4, kvb.KV_F16: 2, kvb.KV_I8: 1}[w.kv_type]
     row = w.shape.num_kv_heads * w.shape.head_dim * esz * 2  # stored K + V bytes per token
     n, tokens = 0, 0
@@ -223,6 +253,8 @@ def main():
             extras["loads_only_us"] = round(loads_only(kvb, dev, part) * 1e3, 2)
         extras["warm_chain_us"] = round(warm_chain(kvb, dev, part) * 1e3, 2)
         extras["warm_gbps"] = round(bytes_step / (extras["warm_chain_us"] * 1e-6) / 1e9, 1)
+        extras["warm_step_us"] = round(warm_steps(kvb, dev, part) * 1e3, 2)
+        extras["empty_step_us"] = round(empty_steps(kvb, w, part) * 1e3, 2)
     keep.append(dev)
     if devi is not None:
         parti = kvb.mi355x_part_tokens(w.shape, wi.max_len,
@@ -266,9 +298,12 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
+        "dtype_detail": "fp32 arithmetic and accumulation; q and p enter the fp16 MFMAs as high/low fp16 pairs "
+                        "(about 22 bits); int8 scores are exact integer MFMAs of the stored bytes with q split "
+                        "into three signed byte digits",
         "data": "synthetic: q, K, V ~ N(0,1) from seeds, K/V stored as %s; shuffled block table over a %gx pool"
                 % ({"f32": "fp32", "f16": "fp16 (RNE)", "i8": "int8 per-(page, KV head) scales"}[storage], cfg["pool"]),
-        "config": {"workload": WORKLOAD_TEXT[args.config] + ", partition %d, cold HBM (1 GiB flush per step)" % part_res,
+        "config": {"workload": WORKLOAD_TEXT[args.config] + ", partition %d, cold (1 GiB read flush per step)" % part_res,
                    "kv_storage": storage, "bytes_per_step": bytes_step, "timed_wall_s": round(wall, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,

@@ -207,13 +207,13 @@ size_t kvb_pipelined_pending(void);
 int kvb_end_pipelined(double* ms, size_t cap, size_t* count);
 
 /* ---- probes ------------------------------------------------------------------------------ */
-/* Streams `bytes` (a multiple of 16) of `dev` once with 128-bit loads over every CU; *ms is the
- * kernel's GPU time (run_read_bandwidth, src/metal_attn.hpp:102). */
+/* Streams `bytes` (a multiple of 16) of `dev` once with non-temporal 128-bit loads over every CU; *ms
+ * is the kernel's GPU time (run_read_bandwidth, src/metal_attn.hpp:102). */
 int kvb_run_read_bandwidth(const void* dev, size_t bytes, double* ms);
-/* Streams a 1 GiB scratch buffer (more than the 256 MB MALL plus the L2s) through the caches so
- * the next timed run starts cold (flush_gpu_caches, src/metal_attn.hpp:106, whose 256 MiB blit
- * fill writes instead: reading evicts as well and leaves no dirty lines to write back during the
- * timed run). */
+/* Reads a 1 GiB scratch buffer (more than the 256 MB MALL plus the L2s) with ordinary loads, which
+ * allocate in those caches, so the next timed run starts cold (flush_gpu_caches,
+ * src/metal_attn.hpp:106, whose 256 MiB blit fill writes instead: reading evicts as well and leaves
+ * no dirty lines to write back during the timed run). */
 int kvb_flush_gpu_caches(void);
 
 #ifdef __cplusplus

@@ -1,0 +1,102 @@
+"""Per-workgroup timelines of one decode step, from the measurement build with workgroup timestamps
+(make -C kv-cache-bench_amd timestamps -> kv-cache-bench_amd/build-ts).
+
+For each BASELINE configuration named on the command line, runs cold steps (1 GiB read flush before
+each) of three launches of paged_decode on the same cache, and summarises their stamps:
+  fused    the step as kvb_run_paged runs it (the partition merge fused in);
+  decode   the same kernel with the merge left to paged_reduce (the two-kernel form's first kernel);
+  loads    the loads-only variant (kvb_run_paged_loads): every K/V load, no arithmetic.
+Stamps (s_memrealtime, 100 MHz, relative to the launch's first workgroup start), per workgroup:
+start, wave 0's loop end, partition stored and acknowledged, merge done. Reported: the event time,
+the span of the stamps, percentiles of starts, loop durations and loop ends, the store time after
+the loop, the merge time of the merging workgroups, and the time from the last loop end to the end.
+Median over 5 launches after 1 discarded. Prints a markdown table per configuration.
+
+usage: python3 kv-cache-bench_amd/bench/wg_timeline.py c2 [c3 c4 c5i8 ...]
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+os.environ["KVB_BUILD_DIR"] = os.path.join(ROOT, "kv-cache-bench_amd", "build-ts")
+sys.path.insert(0, ROOT)
+import __graft_entry__ as graft  # noqa: E402
+
+GROUPS = 65536  # kWgStampGroups in paged_decode_impl.hpp
+COLUMNS = [("event_us", "event"), ("span_us", "stamp span"), ("wgs", "workgroups"), ("start_p50", "start p50"),
+           ("start_max", "start max"), ("loop_p10", "loop p10"), ("loop_p50", "loop p50"), ("loop_p90", "loop p90"),
+           ("loopend_p50", "loop end p50"), ("loopend_max", "loop end max"), ("store_p50", "store p50"),
+           ("mergers", "mergers"), ("merge_p50", "merge p50"), ("tail_us", "last loop end to end")]
+
+
+def summarise(kvb, dev, part, mode, read, reps=6):
+    buf = np.zeros(GROUPS * 4, np.uint64)
+    prev = 0
+    rows = []
+    for rep in range(reps):
+        kvb.flush_gpu_caches()
+        if mode == "fused":
+            ms = dev.run(part)
+        elif mode == "decode":
+            ms = dev.run_split(part)[0]
+        else:
+            ms = dev.run_loads(part)
+        kvb.synchronize()
+        if read(buf.ctypes.data, buf.size) != 0:
+            raise RuntimeError("reading the workgroup stamps failed")
+        ts = buf.reshape(-1, 4).astype(np.int64)
+        valid = ts[:, 0] > prev  # written by this launch (workgroups with no tokens write none)
+        prev = int(ts[:, :3].max())
+        t = ts[valid]
+        base = t[:, 0].min()
+        start, loop_end, stored = ((t[:, i] - base) / 100.0 for i in range(3))
+        merged = t[:, 3] > 0
+        merge_end = (t[merged, 3] - base) / 100.0
+        end = max(stored.max(), merge_end.max() if merged.any() else 0.0)
+        if rep == 0:
+            continue
+        pct = lambda a, q: float(np.percentile(a, q))
+        loop = loop_end - start
+        rows.append({
+            "event_us": ms * 1e3, "span_us": end, "wgs": int(valid.sum()),
+            "start_p50": pct(start, 50), "start_max": float(start.max()),
+            "loop_p10": pct(loop, 10), "loop_p50": pct(loop, 50), "loop_p90": pct(loop, 90),
+            "loopend_p50": pct(loop_end, 50), "loopend_max": float(loop_end.max()),
+            "store_p50": pct(stored - loop_end, 50),
+            "mergers": int(merged.sum()),
+            "merge_p50": pct(merge_end - stored[merged], 50) if merged.any() else 0.0,
+            "tail_us": end - float(loop_end.max()),
+        })
+    return {k: float(np.median([r[k] for r in rows])) for k in rows[0]}
+
+
+def main(configs):
+    kvb = graft.load_package()
+    if not kvb.gpu_available():
+        sys.exit("wg_timeline: no GPU")
+    print(f"device: {kvb.device_name()}; us, relative to the launch's first workgroup start\n")
+    for cfg in configs:
+        w, c, cfgd = kvb.make_config(cfg, threads=16)
+        part = kvb.config_part(cfgd, w)
+        read = getattr(kvb.hip, "kvb_wg_stamps_" + kvb.KV_NAMES[w.kv_type])
+        read.argtypes, read.restype = [ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int
+        dev = kvb.DeviceCase(w, c)
+        print(f"### {cfg}: partition {part}, {int(w.lens.sum())} tokens\n")
+        print("| launch | " + " | ".join(h for _, h in COLUMNS) + " |")
+        print("|---" * (len(COLUMNS) + 1) + "|")
+        for mode in ("fused", "decode", "loads"):
+            r = summarise(kvb, dev, part, mode, read)
+            cells = [f"{r[k]:.0f}" if k in ("wgs", "mergers") else f"{r[k]:.2f}" for k, _ in COLUMNS]
+            print(f"| {mode} | " + " | ".join(cells) + " |", flush=True)
+        print()
+        dev.free()
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:] or ["c2"])

@@ -195,11 +195,19 @@ __global__ __launch_bounds__(256) void attention_fp64_kernel(NaiveParams p, int 
 
 // The streaming-read ceiling (the reference's read_bw, src/kernels.metal:220-233), one workgroup per
 // CU: workgroup g reads the contiguous words [g * per_group, (g + 1) * per_group), kReadBwThreads at
-// a time, kReadBwUnroll non-temporal 16-byte loads in flight per thread (32 KB per workgroup). The
-// words are XOR-accumulated; the store fires only on a sentinel that no buffer the probe reads (all
-// words equal) produces.
+// a time, kReadBwUnroll 16-byte loads in flight per thread (32 KB per workgroup). The words are
+// XOR-accumulated; the store fires only on a sentinel that no buffer the probe reads (all words
+// equal) produces. NT: non-temporal loads, the probe's (fastest); the cache flush uses ordinary
+// loads, which allocate in the L2s and the MALL and so evict what was there.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+template <bool NT>
+__device__ __forceinline__ u32x4_t stream_load(const u32x4_t* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+
+template <bool NT>
 __global__ __launch_bounds__(kReadBwThreads) void read_bw_kernel(const u32x4_t* __restrict__ src, size_t n16,
                                                                  size_t per_group, float* sink) {
     const size_t beg = (size_t)blockIdx.x * per_group;
@@ -210,13 +218,13 @@ __global__ __launch_bounds__(kReadBwThreads) void read_bw_kernel(const u32x4_t* 
     for (; i + (U - 1) * T < end; i += U * T) {
         u32x4_t x[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) x[u] = __builtin_nontemporal_load(src + i + u * T);
+        for (int u = 0; u < U; ++u) x[u] = stream_load<NT>(src + i + u * T);
         __builtin_amdgcn_sched_barrier(0);  // all U loads go out before the first wait
 #pragma unroll
         for (int u = 0; u < U; ++u) acc ^= x[u].x ^ x[u].y ^ x[u].z ^ x[u].w;
     }
     for (; i < end; i += T) {
-        const u32x4_t x = __builtin_nontemporal_load(src + i);
+        const u32x4_t x = stream_load<NT>(src + i);
         acc ^= x.x ^ x.y ^ x.z ^ x.w;
     }
     if (acc == 0x9e3779b9u) sink[((size_t)blockIdx.x * T + threadIdx.x) % kReadBwSink] = 1.0f;
@@ -268,11 +276,16 @@ hipError_t launch_attention_fp64(int kind, int head_dim, int group, const NaiveP
     return hipGetLastError();
 }
 
-hipError_t launch_read_bw(const void* src, size_t n16, int groups, float* sink, hipStream_t s, const Marks& m) {
+hipError_t launch_read_bw(const void* src, size_t n16, int groups, float* sink, hipStream_t s, const Marks& m,
+                          bool nontemporal) {
     if (groups <= 0) return hipErrorInvalidValue;
     const size_t per_group = (n16 + groups - 1) / groups;
-    launch_marked(read_bw_kernel, dim3(groups), dim3(kReadBwThreads), s, m, static_cast<const u32x4_t*>(src), n16,
-                  per_group, sink);
+    if (nontemporal)
+        launch_marked(read_bw_kernel<true>, dim3(groups), dim3(kReadBwThreads), s, m, static_cast<const u32x4_t*>(src),
+                      n16, per_group, sink);
+    else
+        launch_marked(read_bw_kernel<false>, dim3(groups), dim3(kReadBwThreads), s, m, static_cast<const u32x4_t*>(src),
+                      n16, per_group, sink);
     return hipGetLastError();
 }
 

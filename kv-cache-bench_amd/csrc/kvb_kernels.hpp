@@ -66,6 +66,7 @@ struct DecodeParams {
     int page_size;
     FastDiv page_div;           // division by page_size
     int tile_in_page;           // page_size and part_tokens are multiples of 32: a 32-token tile lies in one page
+    int table_in_lanes;         // tile-aligned, and a partition touches at most kLaneBlocks blocks
     int max_blocks;
     int max_parts;
     int part_tokens;
@@ -86,6 +87,10 @@ struct DecodeParams {
     // (tile-aligned pages only: page_size and part_tokens multiples of kTile).
     int loads_only;
 };
+
+// Blocks of one partition that paged_decode holds in lanes: one per lane of one VGPR (and, for int8,
+// one VGPR each for the K and V scales). With more, it reads the block table per tile instead.
+constexpr int kLaneBlocks = 64;
 
 // Ragged batches up to this many sequences use the longest-first work order (one lane per
 // sequence, 8 sequences per lane at most).
@@ -203,7 +208,10 @@ hipError_t launch_attention_fp64(int kind, int head_dim, int group, const NaiveP
 constexpr int kReadBwThreads = 512;
 constexpr int kReadBwUnroll = 4;
 constexpr size_t kReadBwSink = 2048 * 256;
-hipError_t launch_read_bw(const void* src, size_t n16, int groups, float* sink, hipStream_t s, const Marks& m = {});
+// nontemporal: the probe's loads; false: ordinary loads, which allocate in (and so evict) the L2s and
+// the MALL, for the cache flush.
+hipError_t launch_read_bw(const void* src, size_t n16, int groups, float* sink, hipStream_t s, const Marks& m = {},
+                          bool nontemporal = true);
 // Overwrites n16 16-byte words with `value`.
 hipError_t launch_fill(void* dst, size_t n16, uint32_t value, hipStream_t s);
 

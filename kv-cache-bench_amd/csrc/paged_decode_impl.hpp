@@ -80,6 +80,16 @@ constexpr int kTok = 2 * kHalf;    // tokens per wave step (the K of a 16x16x32 
 // streaming reads reach ~7.0 TB/s with it against ~6.3 TB/s without.
 constexpr int kNonTemporal = 2;
 
+#ifdef KVB_WG_TIMESTAMPS
+// Measurement build only (make -C kv-cache-bench_amd timestamps, into build-ts/): per-workgroup
+// s_memrealtime stamps (100 MHz) of the last launch, 4 per linear workgroup id: start, wave 0's loop
+// end, partition stored and acknowledged (loop end again for the loads-only variant), merge done (0
+// where the workgroup did not merge). Read by kvb_wg_stamps_<kind> (paged_decode_<kind>.hip). The
+// stamped build waits for its partition stores before the merge test in the two-kernel form too.
+constexpr unsigned kWgStampGroups = 65536;
+__device__ unsigned long long g_wg_stamps[kWgStampGroups * 4];
+#endif
+
 // ---- cross-lane helpers -------------------------------------------------------------------------
 
 template <int CTRL>
@@ -179,6 +189,8 @@ struct TileRegs {
     uint4 v[2][T::NV];
     // int8: K and V scales of the tokens this lane holds in the score layout (FAST: one per half)
     float ks[KIND == KV_I8 ? 8 : 1], vs[KIND == KV_I8 ? 8 : 1];
+    // FAST with the partition's blocks in lanes: each half's block, relative to the partition's first
+    int rel[2];
 };
 
 // ---- the kernel ---------------------------------------------------------------------------------
@@ -293,12 +305,14 @@ __device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int bat
     return WorkItem{__builtin_amdgcn_readfirstlane(r.b), __builtin_amdgcn_readfirstlane(r.part)};
 }
 
-// (waves_per_eu(2): up to two waves per SIMD, two workgroups per CU, each wave keeping one tile in
-// flight while it computes another; the register budget that leaves is 256 per lane)
+// (waves_per_eu: the register budget. 2 waves per SIMD (two workgroups per CU) leave 256 VGPRs per
+// lane. The tile-aligned int8 kernel is held to 3 (168 VGPRs, no spills), so that three of its
+// workgroups share a CU on multi-round grids; at 169 VGPRs it would drop to two. With one query head
+// per workgroup it would spill there, so that case keeps 2.)
 // LOADS: the measurement variant (kvb_run_paged_loads). It issues every load of the decode in the
 // same order and consumes the registers with XORs, and computes and writes nothing.
 template <int KIND, int D, int QG, bool FAST, bool LOADS = false>
-__global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(KIND == KV_I8 && FAST && !LOADS && QG > 1 ? 3 : 2))) void paged_decode_kernel(DecodeParams p) {
     using T = KvT<KIND, D>;
     using R = TileRegs<KIND, D>;
     constexpr int W = decode_waves(KIND);
@@ -321,6 +335,10 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // every partition's work over all XCDs. With the partition fastest, the XCD followed the
     // partition index, and the partitions that short sequences leave empty left XCDs idle (c5
     // fp16: 486 -> 366 us; equal lengths under a longer max_len ran 1.7x slower).
+#ifdef KVB_WG_TIMESTAMPS
+    const unsigned long long ts0 = __builtin_amdgcn_s_memrealtime();
+    const unsigned lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+#endif
     int part = blockIdx.z, b = blockIdx.y;
     if (p.ragged_items) {
         const WorkItem it = ragged_item(p.seq_lens, p.batch, p.part_tokens, p.len_cap, blockIdx.y, gridDim.y);
@@ -344,12 +362,32 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, q4 = lane >> 4;  // MFMA: column (stack row of q) / token row, row quad
-    // The block table and the int8 scales are read through the constant address space: nothing
-    // writes them during the kernel, and that lets the wave-uniform reads be scalar loads, whose
-    // counter (lgkmcnt) is separate from the K/V loads'. As vector loads, the wait for a block id
-    // (vmcnt counts in order) would also wait for every tile still in flight.
+    // The block table is read through the constant address space: nothing writes it during the
+    // kernel, and that lets the wave-uniform reads be scalar loads, whose counter (lgkmcnt) is
+    // separate from the K/V loads'. As vector loads, the wait for a block id (vmcnt counts in order)
+    // would also wait for every tile still in flight. A block id is waited for as soon as it is read.
+    // The int8 scales are the opposite case: nothing waits for them until the tile's arithmetic, so
+    // they are vector (buffer) loads, counted by vmcnt in order with the tile they belong to, whose
+    // own wait covers them. As scalar loads they were still outstanding when the arithmetic began,
+    // and every LDS wait there (lgkmcnt is shared with scalar loads, which return out of order and so
+    // can only be waited to zero) waited for them as well: with cold caches, an HBM round trip per
+    // tile (c3 int8, measured on MI355X: 48.3 -> see the commit of this change).
     const const_i32 bt = (const_i32)p.block_table + (size_t)b * p.max_blocks;
     const const_f32 ksc = (const_f32)p.k_scale, vsc = (const_f32)p.v_scale;
+    const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.k_scale), (short)0,
+                                                                         0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.v_scale), (short)0,
+                                                                         0x7fffffff, 0x00020000);
+    // FAST, when a partition touches at most kLaneBlocks blocks (p.table_in_lanes): lane i of every
+    // wave holds the id of the partition's (bi0 + i)-th block and, for int8, its K and V scales, loaded
+    // once, here. A tile then takes its block id and scales with v_readlane: no scalar load and wait per
+    // tile in the load path, and no scale load in flight during the arithmetic. (One register per
+    // value: an array indexed at run time would be placed in LDS, a read and a wait per lookup.)
+    const bool lanes = FAST && p.table_in_lanes;
+    const int bi0 = fast_div(t0, p.page_div);
+    int blkv = 0;  // loaded below, after q's loads are issued
+    float ksv = 0.0f, vsv = 0.0f;
+    auto lane_block = [&](int rel) { return __builtin_amdgcn_readlane(blkv, rel); };
     const char* kbase = static_cast<const char*>(p.k);
     const char* vbase = static_cast<const char*>(p.v);
     unsigned char* vt = s_v[wave];
@@ -369,9 +407,11 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                 const int tc = min(th, t1 - 1);
                 if (h == 0 || !p.tile_in_page) {
                     const int bi = fast_div(tc, p.page_div);
-                    braw = bt[bi];
+                    r.rel[h] = bi - bi0;
+                    braw = lanes ? lane_block(bi - bi0) : bt[bi];
                     off = tc - bi * P;
                 } else {
+                    r.rel[h] = r.rel[0];
                     off += kHalf;
                 }
                 const int blk = max(braw, 0);
@@ -391,12 +431,13 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                     r.v[h][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
                                                               rv, (i * (64 / VL) + lane / VL) * D * T::ESZ + (lane % VL) * 16, 0, kNonTemporal));
                 if constexpr (KIND == KV_I8) {
-                    if (h == 0 || !p.tile_in_page) {
-                        r.ks[h] = ksc[(size_t)blk * Hkv + kvh];
-                        r.vs[h] = vsc[(size_t)blk * Hkv + kvh];
-                    } else {
-                        r.ks[h] = r.ks[0];
-                        r.vs[h] = r.vs[0];
+                    // (with tile_in_page the second half's scales are the first half's: the arithmetic
+                    // selects them; copying the register here would wait for its load, and so for
+                    // every tile in flight)
+                    if (!lanes && (h == 0 || !p.tile_in_page)) {
+                        const int soff = (blk * Hkv + kvh) * 4;
+                        r.ks[h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, soff, 0, 0));
+                        r.vs[h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, soff, 0, 0));
                     }
                 }
             } else {
@@ -452,6 +493,16 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     float qv[NJ][QS];                // raw loads only: any use before the barrier below would wait for them
     for (int j = 0; j < NJ; ++j)
         for (int s = 0; s < QS; ++s) qv[j][s] = qp[T::dslot(j, q4, s)];
+    // the partition's blocks (and int8 scales) into lanes: their round trip overlaps q's
+    if (lanes) {
+        const int nb = fast_div(t1 - 1, p.page_div) - bi0 + 1;  // <= kLaneBlocks (host-checked)
+        if (lane < nb) blkv = p.block_table[(size_t)b * p.max_blocks + bi0 + lane];
+        if constexpr (KIND == KV_I8) {
+            const int soff = lane < nb ? (max(blkv, 0) * Hkv + kvh) * 4 : 0;
+            ksv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, soff, 0, 0));
+            vsv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, soff, 0, 0));
+        }
+    }
 
     const int ntiles = (t1 - t0 + kTok - 1) / kTok;
     int it = wave;
@@ -602,8 +653,22 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                 for (int i = 0; i < 4; ++i) S[h][i] = __builtin_fmaf((float)SB[i], wb, (float)SA[i] * wa);
             }
         }
+        // int8, FAST: the scales of the two halves (the first's for both with tile_in_page), from the
+        // lanes that hold them when the partition's scales are in lanes
+        float ksh[2], vsh[2];
+        if (FAST && lanes) {
+            for (int h = 0; h < 2; ++h) {
+                ksh[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ksv), r.rel[h]));
+                vsh[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vsv), r.rel[h]));
+            }
+        } else {
+            ksh[0] = r.ks[0];
+            vsh[0] = r.vs[0];
+            ksh[1] = (FAST && p.tile_in_page) ? r.ks[0] : r.ks[KIND == KV_I8 ? 1 : 0];
+            vsh[1] = (FAST && p.tile_in_page) ? r.vs[0] : r.vs[KIND == KV_I8 ? 1 : 0];
+        }
         if constexpr (KIND == KV_I8) {
-            float vmx = FAST ? fmaxf(r.vs[0], r.vs[1]) : 0.0f;
+            float vmx = FAST ? fmaxf(vsh[0], vsh[1]) : 0.0f;
             if constexpr (!FAST) {
                 for (int j = 0; j < 8; ++j) vmx = fmaxf(vmx, r.vs[j]);
                 vmx = wave_max(vmx);
@@ -623,7 +688,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
             for (int i = 0; i < 4; ++i) {
                 const int j = 4 * h + i;
                 float f = up;
-                if constexpr (KIND == KV_I8) f *= FAST ? r.ks[h] : r.ks[j];
+                if constexpr (KIND == KV_I8) f *= FAST ? ksh[h] : r.ks[j];
                 s[j] = (S[h][i] + dpp<kQuadSwap1>(S[h][i])) * f;
             }
         // Tokens past the partition end score kNegBig; only a partition's last tile has any, so the
@@ -645,7 +710,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
             const float pr = __builtin_amdgcn_exp2f(s[j] - mn);
             psum += pr;
             float pv = pr;
-            if constexpr (KIND == KV_I8) pv *= (FAST ? r.vs[j >> 2] : r.vs[j]) * vdown;
+            if constexpr (KIND == KV_I8) pv *= (FAST ? vsh[j >> 2] : r.vs[j]) * vdown;
             if constexpr (F32) {
                 pb32[j] = hl ? 0.0f : pv;
             } else {
@@ -716,6 +781,15 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         }
     }
 
+#ifdef KVB_WG_TIMESTAMPS
+    const unsigned long long ts1 = __builtin_amdgcn_s_memrealtime();
+    if (LOADS && threadIdx.x == 0 && lin < kWgStampGroups) {
+        g_wg_stamps[4 * lin] = ts0;
+        g_wg_stamps[4 * lin + 1] = ts1;
+        g_wg_stamps[4 * lin + 2] = ts1;
+        g_wg_stamps[4 * lin + 3] = 0;
+    }
+#endif
     if constexpr (LOADS) {  // (never true for real data; keeps the loads live)
         if (lsink == 0x9e3779b9u) p.part_out[threadIdx.x % D] = 1.0f;
         return;
@@ -774,6 +848,15 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         if (p.out && len <= p.part_tokens)  // one partition: this is the output
             *reinterpret_cast<float4*>(p.out + ((size_t)b * H + h0 + eh) * D + 4 * ed) = r;
     }
+#ifdef KVB_WG_TIMESTAMPS
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (threadIdx.x == 0 && lin < kWgStampGroups) {
+        g_wg_stamps[4 * lin] = ts0;
+        g_wg_stamps[4 * lin + 1] = ts1;
+        g_wg_stamps[4 * lin + 2] = __builtin_amdgcn_s_memrealtime();
+        g_wg_stamps[4 * lin + 3] = 0;
+    }
+#endif
     if (!p.out || len <= p.part_tokens) return;
 
     // ---- fused merge (src/kernels.metal:123-147): the last workgroup of this (sequence, head
@@ -846,6 +929,9 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
             write_out();
         }
         if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#ifdef KVB_WG_TIMESTAMPS
+        if (threadIdx.x == 0 && lin < kWgStampGroups) g_wg_stamps[4 * lin + 3] = __builtin_amdgcn_s_memrealtime();
+#endif
         return;
     }
     float4 pre[kPre];
@@ -874,6 +960,9 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         write_out();
     }
     if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#ifdef KVB_WG_TIMESTAMPS
+    if (threadIdx.x == 0 && lin < kWgStampGroups) g_wg_stamps[4 * lin + 3] = __builtin_amdgcn_s_memrealtime();
+#endif
 }
 
 // Dynamic LDS for the loads-only variant so that a CU holds as many of its workgroups as of the

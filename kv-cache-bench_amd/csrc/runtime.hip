@@ -288,6 +288,10 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
         else if (int st = counters_for(a, &p.counters)) return st;
     }
     const bool fast = a->page_size % kvbk::kTile == 0 && part % kvbk::kTile == 0;
+    // blocks one partition touches: part / page when the page divides it (partitions then start on a
+    // page), else at most two more
+    const long long nb_max = part % a->page_size == 0 ? part / a->page_size : part / a->page_size + 2;
+    p.table_in_lanes = fast && nb_max <= kvbk::kLaneBlocks;
     const kvbk::Marks dm{mk.step.start ? mk.step.start : mk.decode.start, fused ? mk.step.stop : mk.decode.stop};
     const kvbk::Marks rm{mk.reduce.start, mk.step.stop ? mk.step.stop : mk.reduce.stop};
     hipError_t e = hipSuccess;
@@ -662,8 +666,11 @@ int kvb_run_read_bandwidth(const void* dev, size_t bytes, double* ms) {
     return finish(e0, e1, ms);
 }
 
-// Reads (not writes) a 1 GiB buffer: that evicts the MALL and the L2s as well, and leaves no dirty
-// lines whose write-back would compete with the next timed run for HBM bandwidth.
+// Reads (not writes) a 1 GiB buffer with ordinary loads: they allocate in the L2s and the 256 MB MALL
+// and so evict what was there, and leave no dirty lines whose write-back would compete with the next
+// timed run for HBM bandwidth. (Non-temporal loads, the probe's, do not evict the MALL: measured on
+// MI355X, a step of the 134 MB c2 cache after such a flush took 26.7 us against 28.0 us after this
+// one, and c3 46.1 against 47.3-48.1; the 537 MB c4 was 82.8 after either.)
 int kvb_flush_gpu_caches(void) {
     if (int st = ensure_device()) return st;
     if (!g.sink) KVB_HIP(hipMalloc(&g.sink, kSinkFloats * sizeof(float)));
@@ -672,7 +679,7 @@ int kvb_flush_gpu_caches(void) {
         const hipError_t e = kvbk::launch_fill(g.flush_buf, kFlushBytes / 16, 0x3f800000u, g.stream);
         if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("flush fill: ") + hipGetErrorString(e));
     }
-    const hipError_t e = kvbk::launch_read_bw(g.flush_buf, kFlushBytes / 16, g.cus, g.sink, g.stream);
+    const hipError_t e = kvbk::launch_read_bw(g.flush_buf, kFlushBytes / 16, g.cus, g.sink, g.stream, {}, false);
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("flush launch: ") + hipGetErrorString(e));
     return KVB_OK;
 }
