@@ -362,16 +362,17 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, q4 = lane >> 4;  // MFMA: column (stack row of q) / token row, row quad
-    // The block table is read through the constant address space: nothing writes it during the
-    // kernel, and that lets the wave-uniform reads be scalar loads, whose counter (lgkmcnt) is
-    // separate from the K/V loads'. As vector loads, the wait for a block id (vmcnt counts in order)
-    // would also wait for every tile still in flight. A block id is waited for as soon as it is read.
-    // The int8 scales are the opposite case: nothing waits for them until the tile's arithmetic, so
-    // they are vector (buffer) loads, counted by vmcnt in order with the tile they belong to, whose
-    // own wait covers them. As scalar loads they were still outstanding when the arithmetic began,
-    // and every LDS wait there (lgkmcnt is shared with scalar loads, which return out of order and so
-    // can only be waited to zero) waited for them as well: with cold caches, an HBM round trip per
-    // tile (c3 int8, measured on MI355X: 48.3 -> see the commit of this change).
+    // Per tile, outside the lanes case below: the block table is read through the constant address
+    // space (nothing writes it during the kernel), so the wave-uniform reads are scalar loads, whose
+    // counter (lgkmcnt) is separate from the K/V loads'. As vector loads, the wait for a block id
+    // (vmcnt counts in order) would also wait for every tile still in flight; a block id is waited
+    // for as soon as it is read. The int8 scales are the opposite case: nothing waits for them until
+    // the tile's arithmetic, so they are vector (buffer) loads, counted by vmcnt in order with the
+    // tile they belong to, whose own wait covers them. As scalar loads they were still outstanding
+    // when the arithmetic began, and every LDS wait there (lgkmcnt is shared with scalar loads, which
+    // return out of order and so can only be waited to zero) waited for them as well: with cold
+    // caches an HBM round trip per tile (c3 int8 on MI355X: 48.3 us per step that way, 46.5 us with
+    // the scales in lanes).
     const const_i32 bt = (const_i32)p.block_table + (size_t)b * p.max_blocks;
     const const_f32 ksc = (const_f32)p.k_scale, vsc = (const_f32)p.v_scale;
     const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.k_scale), (short)0,
