@@ -12,7 +12,12 @@ the span of the stamps, percentiles of starts, loop durations and loop ends, the
 the loop, the merge time of the merging workgroups, and the time from the last loop end to the end.
 Median over 5 launches after 1 discarded. Prints a markdown table per configuration.
 
-usage: python3 kv-cache-bench_amd/bench/wg_timeline.py c2 [c3 c4 c5i8 ...]
+With --where, also where the workgroups ran (wave 0's HW_ID and XCC_ID, stamped by the same build),
+for the last launch of each form: loop durations and loop ends per XCD, and per rank of a workgroup
+among those that ran on the same CU (by start time), which separates a CU's first workgroup from the
+ones that shared or followed it.
+
+usage: python3 kv-cache-bench_amd/bench/wg_timeline.py [--where] c2 [c3 c4 c5i8 ...]
 """
 from __future__ import annotations
 
@@ -28,15 +33,47 @@ os.environ["KVB_BUILD_DIR"] = os.path.join(ROOT, "kv-cache-bench_amd", "build-ts
 sys.path.insert(0, ROOT)
 import __graft_entry__ as graft  # noqa: E402
 
-GROUPS = 65536  # kWgStampGroups in paged_decode_impl.hpp
+GROUPS, WORDS = 65536, 5  # kWgStampGroups, kWgStampWords in paged_decode_impl.hpp
 COLUMNS = [("event_us", "event"), ("span_us", "stamp span"), ("wgs", "workgroups"), ("start_p50", "start p50"),
            ("start_max", "start max"), ("loop_p10", "loop p10"), ("loop_p50", "loop p50"), ("loop_p90", "loop p90"),
            ("loopend_p50", "loop end p50"), ("loopend_max", "loop end max"), ("store_p50", "store p50"),
            ("mergers", "mergers"), ("merge_p50", "merge p50"), ("tail_us", "last loop end to end")]
 
 
-def summarise(kvb, dev, part, mode, read, reps=6):
-    buf = np.zeros(GROUPS * 4, np.uint64)
+def where_tables(t, start, loop_end):
+    """Loop durations and ends by XCD and by a workgroup's rank on its CU, as markdown rows."""
+    hw = (t[:, 4] & 0xFFFFFFFF).astype(np.int64)
+    xcc = (t[:, 4] >> 32).astype(np.int64) & 0xF
+    cu = (xcc << 16) | (((hw >> 13) & 7) << 8) | (((hw >> 12) & 1) << 4) | ((hw >> 8) & 15)
+    loop = loop_end - start
+    order = np.lexsort((start, cu))
+    rank = np.zeros(len(cu), np.int64)
+    prev, r = -1, 0
+    for i in order:
+        r = r + 1 if cu[i] == prev else 0
+        rank[i], prev = r, cu[i]
+    lines = [f"{len(np.unique(cu))} CUs used; per XCD:", "",
+             "| XCD | workgroups | start p50 | loop p10 | loop p50 | loop p90 | loop end p50 | loop end max |",
+             "|---|---|---|---|---|---|---|---|"]
+    pct = lambda a, q: float(np.percentile(a, q))
+    for x in np.unique(xcc):
+        m = xcc == x
+        lines.append(f"| {x} | {int(m.sum())} | {pct(start[m], 50):.2f} | {pct(loop[m], 10):.2f} | "
+                     f"{pct(loop[m], 50):.2f} | {pct(loop[m], 90):.2f} | {pct(loop_end[m], 50):.2f} | "
+                     f"{float(loop_end[m].max()):.2f} |")
+    lines += ["", "per rank on the CU (0 = the CU's first workgroup):", "",
+              "| rank | workgroups | start p50 | loop p10 | loop p50 | loop p90 | loop end p50 | loop end max |",
+              "|---|---|---|---|---|---|---|---|"]
+    for k in np.unique(rank):
+        m = rank == k
+        lines.append(f"| {k} | {int(m.sum())} | {pct(start[m], 50):.2f} | {pct(loop[m], 10):.2f} | "
+                     f"{pct(loop[m], 50):.2f} | {pct(loop[m], 90):.2f} | {pct(loop_end[m], 50):.2f} | "
+                     f"{float(loop_end[m].max()):.2f} |")
+    return lines
+
+
+def summarise(kvb, dev, part, mode, read, reps=6, where=None):
+    buf = np.zeros(GROUPS * WORDS, np.uint64)
     prev = 0
     rows = []
     for rep in range(reps):
@@ -50,7 +87,7 @@ def summarise(kvb, dev, part, mode, read, reps=6):
         kvb.synchronize()
         if read(buf.ctypes.data, buf.size) != 0:
             raise RuntimeError("reading the workgroup stamps failed")
-        ts = buf.reshape(-1, 4).astype(np.int64)
+        ts = buf.reshape(-1, WORDS).astype(np.int64)
         valid = ts[:, 0] > prev  # written by this launch (workgroups with no tokens write none)
         prev = int(ts[:, :3].max())
         t = ts[valid]
@@ -61,6 +98,8 @@ def summarise(kvb, dev, part, mode, read, reps=6):
         end = max(stored.max(), merge_end.max() if merged.any() else 0.0)
         if rep == 0:
             continue
+        if where is not None and rep == reps - 1:
+            where[:] = where_tables(t, start, loop_end)
         pct = lambda a, q: float(np.percentile(a, q))
         loop = loop_end - start
         rows.append({
@@ -76,7 +115,9 @@ def summarise(kvb, dev, part, mode, read, reps=6):
     return {k: float(np.median([r[k] for r in rows])) for k in rows[0]}
 
 
-def main(configs):
+def main(args):
+    show_where = "--where" in args
+    configs = [a for a in args if a != "--where"] or ["c2"]
     kvb = graft.load_package()
     if not kvb.gpu_available():
         sys.exit("wg_timeline: no GPU")
@@ -90,13 +131,19 @@ def main(configs):
         print(f"### {cfg}: partition {part}, {int(w.lens.sum())} tokens\n")
         print("| launch | " + " | ".join(h for _, h in COLUMNS) + " |")
         print("|---" * (len(COLUMNS) + 1) + "|")
+        wheres = {}
         for mode in ("fused", "decode", "loads"):
-            r = summarise(kvb, dev, part, mode, read)
+            wheres[mode] = []
+            r = summarise(kvb, dev, part, mode, read, where=wheres[mode] if show_where else None)
             cells = [f"{r[k]:.0f}" if k in ("wgs", "mergers") else f"{r[k]:.2f}" for k, _ in COLUMNS]
             print(f"| {mode} | " + " | ".join(cells) + " |", flush=True)
         print()
+        for mode, lines in wheres.items():
+            if lines:
+                print(f"#### {cfg}, {mode}: where the workgroups ran (last launch)\n")
+                print("\n".join(lines) + "\n", flush=True)
         dev.free()
 
 
 if __name__ == "__main__":
-    main(sys.argv[1:] or ["c2"])
+    main(sys.argv[1:])

@@ -12,9 +12,10 @@ hipError_t launch_paged_decode_f32(int head_dim, int qg, bool fast, const Decode
 }  // namespace kvbk
 
 #ifdef KVB_WG_TIMESTAMPS
-// Measurement build only: copies n stamps (4 per workgroup) of this storage type's last launch.
+// Measurement build only: copies n stamp words (kWgStampWords per workgroup) of this storage type's
+// last launch.
 extern "C" int kvb_wg_stamps_f32(void* dst, size_t n) {
-    if (n > kvbk::kWgStampGroups * 4) return (int)hipErrorInvalidValue;
+    if (n > kvbk::kWgStampGroups * kvbk::kWgStampWords) return (int)hipErrorInvalidValue;
     return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(kvbk::g_wg_stamps), n * sizeof(unsigned long long), 0,
                                     hipMemcpyDeviceToHost);
 }

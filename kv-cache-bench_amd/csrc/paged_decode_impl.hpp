@@ -82,12 +82,18 @@ constexpr int kNonTemporal = 2;
 
 #ifdef KVB_WG_TIMESTAMPS
 // Measurement build only (make -C kv-cache-bench_amd timestamps, into build-ts/): per-workgroup
-// s_memrealtime stamps (100 MHz) of the last launch, 4 per linear workgroup id: start, wave 0's loop
-// end, partition stored and acknowledged (loop end again for the loads-only variant), merge done (0
-// where the workgroup did not merge). Read by kvb_wg_stamps_<kind> (paged_decode_<kind>.hip). The
-// stamped build waits for its partition stores before the merge test in the two-kernel form too.
-constexpr unsigned kWgStampGroups = 65536;
-__device__ unsigned long long g_wg_stamps[kWgStampGroups * 4];
+// s_memrealtime stamps (100 MHz) of the last launch, kWgStampWords per linear workgroup id: start,
+// wave 0's loop end, partition stored and acknowledged (loop end again for the loads-only variant),
+// merge done (0 where the workgroup did not merge), and where wave 0 ran: HW_ID (SIMD, CU, SH, SE) in
+// the low 32 bits, XCC_ID above. Read by kvb_wg_stamps_<kind> (paged_decode_<kind>.hip). The stamped
+// build waits for its partition stores before the merge test in the two-kernel form too.
+constexpr unsigned kWgStampGroups = 65536, kWgStampWords = 5;
+__device__ unsigned long long g_wg_stamps[kWgStampGroups * kWgStampWords];
+__device__ __forceinline__ unsigned long long wg_where() {
+    const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);    // hwreg(HW_REG_HW_ID)
+    const unsigned xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);  // hwreg(HW_REG_XCC_ID)
+    return ((unsigned long long)xcc << 32) | hw;
+}
 #endif
 
 // ---- cross-lane helpers -------------------------------------------------------------------------
@@ -785,10 +791,12 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
 #ifdef KVB_WG_TIMESTAMPS
     const unsigned long long ts1 = __builtin_amdgcn_s_memrealtime();
     if (LOADS && threadIdx.x == 0 && lin < kWgStampGroups) {
-        g_wg_stamps[4 * lin] = ts0;
-        g_wg_stamps[4 * lin + 1] = ts1;
-        g_wg_stamps[4 * lin + 2] = ts1;
-        g_wg_stamps[4 * lin + 3] = 0;
+        unsigned long long* st = g_wg_stamps + kWgStampWords * lin;
+        st[0] = ts0;
+        st[1] = ts1;
+        st[2] = ts1;
+        st[3] = 0;
+        st[4] = wg_where();
     }
 #endif
     if constexpr (LOADS) {  // (never true for real data; keeps the loads live)
@@ -852,10 +860,12 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
 #ifdef KVB_WG_TIMESTAMPS
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (threadIdx.x == 0 && lin < kWgStampGroups) {
-        g_wg_stamps[4 * lin] = ts0;
-        g_wg_stamps[4 * lin + 1] = ts1;
-        g_wg_stamps[4 * lin + 2] = __builtin_amdgcn_s_memrealtime();
-        g_wg_stamps[4 * lin + 3] = 0;
+        unsigned long long* st = g_wg_stamps + kWgStampWords * lin;
+        st[0] = ts0;
+        st[1] = ts1;
+        st[2] = __builtin_amdgcn_s_memrealtime();
+        st[3] = 0;
+        st[4] = wg_where();
     }
 #endif
     if (!p.out || len <= p.part_tokens) return;
@@ -931,7 +941,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         }
         if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef KVB_WG_TIMESTAMPS
-        if (threadIdx.x == 0 && lin < kWgStampGroups) g_wg_stamps[4 * lin + 3] = __builtin_amdgcn_s_memrealtime();
+        if (threadIdx.x == 0 && lin < kWgStampGroups) g_wg_stamps[kWgStampWords * lin + 3] = __builtin_amdgcn_s_memrealtime();
 #endif
         return;
     }
@@ -962,7 +972,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     }
     if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef KVB_WG_TIMESTAMPS
-    if (threadIdx.x == 0 && lin < kWgStampGroups) g_wg_stamps[4 * lin + 3] = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0 && lin < kWgStampGroups) g_wg_stamps[kWgStampWords * lin + 3] = __builtin_amdgcn_s_memrealtime();
 #endif
 }
 
