@@ -186,6 +186,8 @@ def main():
     ap.add_argument("--config", default="c4", choices=sorted(WORKLOAD_TEXT))
     ap.add_argument("--part", type=int, default=None,
                     help="partition tokens (default: the config's, else the MI355X policy; 0 = auto_part_tokens)")
+    ap.add_argument("--pair", choices=["auto", "off", "always"], default="auto",
+                    help="two partitions per decode workgroup (kvb_set_pair_mode); the same bits either way")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the two-kernel, warm, probe and (c4) int8 measurements")
@@ -200,6 +202,7 @@ def main():
         print("bench.py: no GPU", file=sys.stderr)
         sys.exit(1)
     log(f"device: {kvb.device_name()}")
+    kvb.set_pair_mode(args.pair)
     # The probe runs first, and nothing is freed until every GPU measurement is done: on these boxes
     # kernels run measurably slower for a while after a large hipFree (the same 4 GiB buffer read
     # 7.05 TB/s before and 6.7 TB/s after other buffers were freed).

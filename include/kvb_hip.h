@@ -144,6 +144,18 @@ int kvb_run_paged_split(const kvb_paged_args* a, double* decode_ms, double* redu
  * the decode's memory traffic alone, which bounds the decode kernel from below. Same refusals as
  * kvb_run_paged, plus KVB_EINVAL unless page_size and the partition are multiples of 16. */
 int kvb_run_paged_loads(const kvb_paged_args* a, double* ms);
+/* Tuning switch, not in the reference: when a decode workgroup computes two consecutive partitions
+ * instead of one. KVB_PAIR_AUTO (the default): when the plain (sequence, partition) grid would put
+ * two or more workgroups on every CU; KVB_PAIR_OFF: never; KVB_PAIR_ALWAYS: whenever it is allowed.
+ * It is allowed for f16 and i8 caches with page_size and the partition multiples of 16, the
+ * partition a multiple of 128, at least two partitions, and equal lengths (or one sequence). Every
+ * setting gives the same bits: each partition is computed by the same waves, in the same order.
+ * Returns the previous setting, or -1 for an unknown one (nothing changed). Applies to every later
+ * decode step of the process. */
+#define KVB_PAIR_AUTO 0
+#define KVB_PAIR_OFF 1
+#define KVB_PAIR_ALWAYS 2
+int kvb_set_pair_mode(int mode);
 
 /* ---- cache writers on the GPU --------------------------------------------------------------
  * The producers of the paged cache the decode reads, as the reference runs them on the host:

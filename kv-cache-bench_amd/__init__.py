@@ -90,6 +90,7 @@ _SIGS = {
     "kvb_run_paged_steps": ([_PA, _i, _d], _i),
     "kvb_run_paged_split": ([_PA, _d, _d], _i),
     "kvb_run_paged_loads": ([_PA, _d], _i),
+    "kvb_set_pair_mode": ([_i], _i),
     "kvb_run_paged_noalloc": ([_PA], _i),
     "kvb_run_naive": ([_NA, _d], _i),
     "kvb_check_naive": ([_NA], _i),
@@ -489,6 +490,18 @@ def flush_gpu_caches():
 
 def synchronize():
     check(hip.kvb_synchronize(), "synchronize")
+
+
+PAIR_MODES = {"auto": 0, "off": 1, "always": 2}
+
+
+def set_pair_mode(mode: str) -> str:
+    """When a decode workgroup computes two consecutive partitions (kvb_set_pair_mode): "auto",
+    "off" or "always" (where allowed). Returns the previous mode."""
+    prev = hip.kvb_set_pair_mode(PAIR_MODES[mode])
+    if prev < 0:
+        raise KvbInvalidArgument(f"set_pair_mode: unknown mode {mode!r}")
+    return {v: k for k, v in PAIR_MODES.items()}[prev]
 
 
 def set_stream(stream):

@@ -86,6 +86,11 @@ struct DecodeParams {
     // Nonzero: launch the measurement variant that issues the decode's loads and computes nothing
     // (tile-aligned pages only: page_size and part_tokens multiples of kTile).
     int loads_only;
+    // Nonzero: each workgroup computes two consecutive partitions (the PAIR kernels). Requires
+    // tile-aligned pages, an f16 or i8 cache, the plain grid (ragged_items 0), and part_tokens a
+    // multiple of 2 * kTile * decode_waves(kind) (32-token tiles, dealt round robin to the waves), so
+    // that each partition keeps its tiles' waves and order.
+    int pair;
 };
 
 // Blocks of one partition that paged_decode holds in lanes: one per lane of one VGPR (and, for int8,

@@ -314,11 +314,17 @@ __device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int bat
 // (waves_per_eu: the register budget. 2 waves per SIMD (two workgroups per CU) leave 256 VGPRs per
 // lane. The tile-aligned int8 kernel is held to 3 (168 VGPRs, no spills), so that three of its
 // workgroups share a CU on multi-round grids; at 169 VGPRs it would drop to two. With one query head
-// per workgroup it would spill there, so that case keeps 2.)
+// per workgroup it would spill there, so that case keeps 2, as do the PAIR kernels, which run one
+// workgroup per CU.)
 // LOADS: the measurement variant (kvb_run_paged_loads). It issues every load of the decode in the
 // same order and consumes the registers with XORs, and computes and writes nothing.
-template <int KIND, int D, int QG, bool FAST, bool LOADS = false>
-__global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(KIND == KV_I8 && FAST && !LOADS && QG > 1 ? 3 : 2))) void paged_decode_kernel(DecodeParams p) {
+// PAIR: a workgroup computes two consecutive partitions (grid z = ceil(max_parts / 2)), so that a grid
+// of two or more workgroups per CU runs as one per CU (DecodeParams::pair). Its waves walk the two
+// partitions' tiles in order; each partition's tiles go to the same waves, in the same order, as in
+// a workgroup of its own (part_tokens is a multiple of 32 * waves), and a wave starts its second
+// partition from a fresh state, so every partition gets the same bits either way.
+template <int KIND, int D, int QG, bool FAST, bool LOADS = false, bool PAIR = false>
+__global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(KIND == KV_I8 && FAST && !LOADS && !PAIR && QG > 1 ? 3 : 2))) void paged_decode_kernel(DecodeParams p) {
     using T = KvT<KIND, D>;
     using R = TileRegs<KIND, D>;
     constexpr int W = decode_waves(KIND);
@@ -335,6 +341,10 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     static_assert(QG * 4 <= kTok * T::LDS_ESZ, "merge buffer must fit in the V tile");
     __shared__ __attribute__((aligned(16))) unsigned char s_v[W][kTok * D * T::LDS_ESZ];
     __shared__ float2 s_ml[W][QG];
+    // PAIR: each wave's state for the first partition, [QG][D] fp32 and (m, l), as the V tile holds
+    // the last partition's after the walk
+    __shared__ __attribute__((aligned(16))) float s_part[PAIR ? W : 1][PAIR ? QG * D : 4];
+    __shared__ float2 s_ml2[PAIR ? W : 1][QG];
 
     // Grid (H / QG, B, max_parts), head group fastest: workgroups go to the 8 XCDs round robin by
     // linear id, so consecutive ids (one partition of consecutive head groups and sequences) spread
@@ -345,7 +355,8 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     const unsigned long long ts0 = __builtin_amdgcn_s_memrealtime();
     const unsigned lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
 #endif
-    int part = blockIdx.z, b = blockIdx.y;
+    constexpr int G = PAIR ? 2 : 1;  // partitions per workgroup
+    int part = blockIdx.z * G, b = blockIdx.y;  // part: the workgroup's first partition
     if (p.ragged_items) {
         const WorkItem it = ragged_item(p.seq_lens, p.batch, p.part_tokens, p.len_cap, blockIdx.y, gridDim.y);
         if (it.b < 0 || it.b >= p.batch || it.part >= p.max_parts) return;  // uniform, before any barrier
@@ -362,7 +373,8 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
             for (int idx = threadIdx.x; idx < QG * D; idx += 64 * W) p.out[((size_t)b * H + h0) * D + idx] = 0.0f;
         return;
     }
-    const int t1 = min(len, t0 + p.part_tokens);
+    const int t1 = min(len, t0 + G * p.part_tokens);
+    const int ng = PAIR ? (t1 - t0 + p.part_tokens - 1) / p.part_tokens : 1;  // partitions holding tokens
     const int kvh = h0 / p.group;
 
     const int lane = threadIdx.x & 63;
@@ -776,6 +788,29 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // score (p = 0, corr = 1 exactly), reads zeros or masked rows, and at most renormalises the
     // int8 accumulators by a power of two, so it changes nothing. (sched_barrier: the scheduler
     // would otherwise sink part of the prefetch below the wait for the tile being computed.)
+    // ---- the wave's state -> LDS: [QG][D] fp32 (a high-column lane (hl == 0) holds d = 16 mb +
+    // 4 q4 + i (i < 4) of head hh, one 16-byte chunk per mb; chunk c of head h's row is stored at
+    // c ^ (h & 7) so that the 8 heads' rows do not all start in the same LDS banks) and (m, l).
+    // `live`: false writes an empty state (a wave with no tile in that partition).
+    auto state_to_lds = [&](float* dst, float2* dml, bool live) {
+        const float vupf = KIND == KV_I8 ? ldexpf(1.0f, ve) : 1.0f;
+        const float lsum = sum_x16_x32(l);
+        for (int mb = 0; mb < NMB; ++mb) {
+            float4 o4;  // high + low columns
+            o4.x = (acc[mb][0] + dpp<kQuadSwap1>(acc[mb][0])) * vupf;
+            o4.y = (acc[mb][1] + dpp<kQuadSwap1>(acc[mb][1])) * vupf;
+            o4.z = (acc[mb][2] + dpp<kQuadSwap1>(acc[mb][2])) * vupf;
+            o4.w = (acc[mb][3] + dpp<kQuadSwap1>(acc[mb][3])) * vupf;
+            if (!live) o4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (hl == 0 && qcol) *reinterpret_cast<float4*>(dst + hh * D + 4 * ((4 * mb + q4) ^ (hh & 7))) = o4;
+        }
+        if (hl == 0 && qcol && q4 == 0) dml[hh] = live ? make_float2(m, lsum) : make_float2(kNegBig, 0.0f);
+    };
+
+    // PAIR: `cur` is the partition of the range (0 or 1) the wave's state belongs to. At its first
+    // tile of the second partition the wave moves its state to s_part and starts afresh.
+    int cur = 0;
+    const int tpp = p.part_tokens / kTok;  // tiles per partition
     const int wtiles = it < ntiles ? (ntiles - it + W - 1) / W : 0;
     const int rounds = (wtiles + NBUF - 1) / NBUF;
     for (int rd = 0; rd < rounds; ++rd) {
@@ -783,6 +818,17 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         for (int k = 0; k < NBUF; ++k) {
             load_tile(r[(k + NBUF - 1) % NBUF], t0 + (it + (NBUF - 1) * W) * kTok);
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (PAIR && !LOADS) {
+                if (cur == 0 && it >= tpp && it < ntiles) {  // wave-uniform
+                    state_to_lds(s_part[wave], s_ml2[wave], true);
+                    m = kNegBig;
+                    l = 0.0f;
+                    for (int mb = 0; mb < NMB; ++mb) acc[mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                    ve = -160;
+                    vdown = 1.0f;
+                    cur = 1;
+                }
+            }
             compute_tile(r[k], t0 + it * kTok);
             it += W;
         }
@@ -804,47 +850,49 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         return;
     }
 
-    // ---- merge: lanes -> wave state -> workgroup
-    const float vupf = KIND == KV_I8 ? ldexpf(1.0f, ve) : 1.0f;
-    l = sum_x16_x32(l);
-    // The wave's accumulators go to its V tile as [QG][D] fp32: a high-column lane (hl == 0) holds
-    // d = 16 mb + 4 q4 + i (i < 4) of head hh, one 16-byte chunk per mb, and chunk c of head h's row
-    // is stored at c ^ (h & 7) so that the 8 heads' rows do not all start in the same LDS banks.
+    // ---- merge: lanes -> wave state -> workgroup. The wave's last state goes to its V tile (the
+    // range's last partition); PAIR, a wave that never reached the second partition: its state is
+    // the first's, and the second gets an empty one.
     float* sacc = reinterpret_cast<float*>(vt);
-    for (int mb = 0; mb < NMB; ++mb) {
-        float4 o4;  // high + low columns
-        o4.x = (acc[mb][0] + dpp<kQuadSwap1>(acc[mb][0])) * vupf;
-        o4.y = (acc[mb][1] + dpp<kQuadSwap1>(acc[mb][1])) * vupf;
-        o4.z = (acc[mb][2] + dpp<kQuadSwap1>(acc[mb][2])) * vupf;
-        o4.w = (acc[mb][3] + dpp<kQuadSwap1>(acc[mb][3])) * vupf;
-        if (hl == 0 && qcol) *reinterpret_cast<float4*>(sacc + hh * D + 4 * ((4 * mb + q4) ^ (hh & 7))) = o4;
+    bool last_live = true;
+    if constexpr (PAIR) {
+        if (ng == 2 && cur == 0) {  // wave-uniform
+            state_to_lds(s_part[wave], s_ml2[wave], true);
+            last_live = false;
+        }
     }
-    if (hl == 0 && qcol && q4 == 0) s_ml[wave][hh] = make_float2(m, l);
+    state_to_lds(sacc, s_ml[wave], last_live);
     __syncthreads();
 
     // The partition's result: thread e owns the 16-byte chunk ed of head eh. It weighs the waves'
     // states once, sums them in wave order, and writes the chunk with one agent-scope (sc1) store,
     // which writes through this XCD's L2 to the device coherence point, where the merging workgroup,
     // on whichever XCD, reads it.
+    // PAIR: the same for each of the range's partitions (the first's states in s_part).
     static_assert(QG * D / 4 <= 64 * W, "one 16-byte output chunk per thread");
-    if (threadIdx.x < QG * D / 4) {
+    for (int gp = 0; gp < ng; ++gp) {  // uniform
+      const bool lastp = gp == ng - 1;
+      if (threadIdx.x < QG * D / 4) {
         const int eh = threadIdx.x / (D / 4), ed = threadIdx.x % (D / 4);
+        auto wml = [&](int w) { return lastp ? s_ml[w][eh] : s_ml2[PAIR ? w : 0][eh]; };
+        auto wacc = [&](int w) {
+            return lastp ? reinterpret_cast<const float*>(s_v[w]) : &s_part[PAIR ? w : 0][0];
+        };
         float M = kNegBig;
-        for (int w = 0; w < W; ++w) M = fmaxf(M, s_ml[w][eh].x);
+        for (int w = 0; w < W; ++w) M = fmaxf(M, wml(w).x);
         float L = 0.0f;
         float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         for (int w = 0; w < W; ++w) {
-            const float wt = __builtin_amdgcn_exp2f(s_ml[w][eh].x - M);
-            L += s_ml[w][eh].y * wt;
-            const float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(s_v[w]) + eh * D +
-                                                              4 * (ed ^ (eh & 7)));
+            const float wt = __builtin_amdgcn_exp2f(wml(w).x - M);
+            L += wml(w).y * wt;
+            const float4 v = *reinterpret_cast<const float4*>(wacc(w) + eh * D + 4 * (ed ^ (eh & 7)));
             o.x = __builtin_fmaf(v.x, wt, o.x);
             o.y = __builtin_fmaf(v.y, wt, o.y);
             o.z = __builtin_fmaf(v.z, wt, o.z);
             o.w = __builtin_fmaf(v.w, wt, o.w);
         }
         const float4 r = make_float4(o.x / L, o.y / L, o.z / L, o.w / L);
-        const size_t slot0 = ((size_t)b * H + h0) * p.max_parts + part;  // head h0's slot
+        const size_t slot0 = ((size_t)b * H + h0) * p.max_parts + part + gp;  // head h0's slot
         const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(
             p.part_out + slot0 * D, (short)0, QG * p.max_parts * D * 4, 0x00020000);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, r), rpo,
@@ -856,6 +904,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         }
         if (p.out && len <= p.part_tokens)  // one partition: this is the output
             *reinterpret_cast<float4*>(p.out + ((size_t)b * H + h0 + eh) * D + 4 * ed) = r;
+      }
     }
 #ifdef KVB_WG_TIMESTAMPS
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -871,7 +920,8 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     if (!p.out || len <= p.part_tokens) return;
 
     // ---- fused merge (src/kernels.metal:123-147): the last workgroup of this (sequence, head
-    // group) to arrive weighs the partitions by w_i = l_i exp(m_i - M), in paged_reduce's order
+    // group) to arrive (the counter counts partitions: each workgroup adds the ng it wrote) weighs
+    // the partitions by w_i = l_i exp(m_i - M), in paged_reduce's order
     // (the two give identical bits). Message passing without whole-cache fences: each wave waits
     // until its write-through partition stores are acknowledged (s_waitcnt vmcnt(0); __syncthreads
     // alone does not wait for stores), the barrier orders that before thread 0's count (an
@@ -884,7 +934,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nparts - 1;
+        s_last = __hip_atomic_fetch_add(counter, ng, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nparts - ng;
     __syncthreads();
     if (!s_last) return;
 
@@ -981,16 +1031,16 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
 // whenever the grid has more than one per CU. The largest size at which the occupancy calculator
 // gives the variant the decode's count (at most what one workgroup may allocate); computed once per
 // instantiation.
-template <int KIND, int D, int QG>
+template <int KIND, int D, int QG, bool PAIR>
 hipError_t loads_only_lds(size_t* lds) {
     static size_t cached = SIZE_MAX;
     if (cached == SIZE_MAX) {
-        const auto loads = paged_decode_kernel<KIND, D, QG, true, true>;
+        const auto loads = paged_decode_kernel<KIND, D, QG, true, true, PAIR>;
         const int threads = 64 * decode_waves(KIND);
         int occ = 0, dev = 0, lds_cu = 0, lds_wg = 0;
         hipFuncAttributes fa{};
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, paged_decode_kernel<KIND, D, QG, true, false>,
-                                                                    threads, 0);
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &occ, paged_decode_kernel<KIND, D, QG, true, false, PAIR>, threads, 0);
         if (e == hipSuccess) e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_wg, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
@@ -1015,31 +1065,44 @@ hipError_t loads_only_lds(size_t* lds) {
     return hipSuccess;
 }
 
-template <int KIND, int D, int QG, bool FAST>
+template <int KIND, int D, int QG, bool FAST, bool PAIR>
 hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
-    const dim3 grid(p.num_heads / QG, p.ragged_items ? p.ragged_items : batch, p.ragged_items ? 1 : p.max_parts);
+    const int gz = PAIR ? (p.max_parts + 1) / 2 : p.max_parts;
+    const dim3 grid(p.num_heads / QG, p.ragged_items ? p.ragged_items : batch, p.ragged_items ? 1 : gz);
     if (p.loads_only) {  // tile-aligned pages only
         if constexpr (!FAST) {
             return hipErrorInvalidValue;
         } else {
             size_t lds = 0;
-            if (const hipError_t e = loads_only_lds<KIND, D, QG>(&lds); e != hipSuccess) return e;
-            launch_marked_lds(paged_decode_kernel<KIND, D, QG, true, true>, grid, dim3(64 * decode_waves(KIND)), lds, s,
-                              m, p);
+            if (const hipError_t e = loads_only_lds<KIND, D, QG, PAIR>(&lds); e != hipSuccess) return e;
+            launch_marked_lds(paged_decode_kernel<KIND, D, QG, true, true, PAIR>, grid, dim3(64 * decode_waves(KIND)),
+                              lds, s, m, p);
         }
     } else {
-        launch_marked(paged_decode_kernel<KIND, D, QG, FAST>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
+        launch_marked(paged_decode_kernel<KIND, D, QG, FAST, false, PAIR>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
     }
     return hipGetLastError();
+}
+
+// Two partitions per workgroup (DecodeParams::pair): tile-aligned f16 and i8 caches, plain grid only.
+template <int KIND, int D, int QG>
+hipError_t launch_qg(bool fast, const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
+    if (!fast) return p.pair ? hipErrorInvalidValue : launch_one<KIND, D, QG, false, false>(p, batch, s, m);
+    if constexpr (KIND != KV_F32) {
+        if (p.pair) return p.ragged_items ? hipErrorInvalidValue : launch_one<KIND, D, QG, true, true>(p, batch, s, m);
+    } else {
+        if (p.pair) return hipErrorInvalidValue;
+    }
+    return launch_one<KIND, D, QG, true, false>(p, batch, s, m);
 }
 
 template <int KIND, int D>
 hipError_t launch_for_dim(int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
     switch (qg) {
-        case 1: return fast ? launch_one<KIND, D, 1, true>(p, batch, s, m) : launch_one<KIND, D, 1, false>(p, batch, s, m);
-        case 2: return fast ? launch_one<KIND, D, 2, true>(p, batch, s, m) : launch_one<KIND, D, 2, false>(p, batch, s, m);
-        case 4: return fast ? launch_one<KIND, D, 4, true>(p, batch, s, m) : launch_one<KIND, D, 4, false>(p, batch, s, m);
-        case 8: return fast ? launch_one<KIND, D, 8, true>(p, batch, s, m) : launch_one<KIND, D, 8, false>(p, batch, s, m);
+        case 1: return launch_qg<KIND, D, 1>(fast, p, batch, s, m);
+        case 2: return launch_qg<KIND, D, 2>(fast, p, batch, s, m);
+        case 4: return launch_qg<KIND, D, 4>(fast, p, batch, s, m);
+        case 8: return launch_qg<KIND, D, 8>(fast, p, batch, s, m);
         default: return hipErrorInvalidValue;
     }
 }

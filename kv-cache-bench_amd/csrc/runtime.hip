@@ -44,6 +44,7 @@ struct Runtime {
     void* flush_buf = nullptr;      // cache-flush source
     hipEvent_t switch_ev = nullptr; // orders a new stream after the old one (kvb_set_stream)
     int cus = 0;                    // compute units: the read probe runs one workgroup per CU
+    int pair_mode = KVB_PAIR_AUTO;  // kvb_set_pair_mode
     float* sink = nullptr;          // read-probe sink
     bool pipelined = false;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> timed;
@@ -288,9 +289,18 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
         else if (int st = counters_for(a, &p.counters)) return st;
     }
     const bool fast = a->page_size % kvbk::kTile == 0 && part % kvbk::kTile == 0;
-    // blocks one partition touches: part / page when the page divides it (partitions then start on a
-    // page), else at most two more
-    const long long nb_max = part % a->page_size == 0 ? part / a->page_size : part / a->page_size + 2;
+    // Two partitions per workgroup when the plain grid holds two or more workgroups per CU: the two
+    // workgroups sharing a CU do not share it evenly (the first ends its loop long before the second,
+    // which then streams alone); one workgroup per CU was faster (c2 on MI355X, 512 workgroups of 512
+    // tokens: 28.3 us per step, against 26.5 us for 256 workgroups of 1024 tokens).
+    const long long wgs = (long long)a->batch * (a->num_heads / qg) * p.max_parts;
+    p.pair = fast && a->kv_type != KVB_KV_F32 && !p.ragged_items && p.max_parts >= 2 &&
+             part % (2 * kvbk::kTile * kvbk::decode_waves(a->kv_type)) == 0 &&
+             (g.pair_mode == KVB_PAIR_ALWAYS || (g.pair_mode == KVB_PAIR_AUTO && wgs >= 2LL * g.cus));
+    // blocks one workgroup's range touches: its tokens / page when the page divides them (the range
+    // then starts on a page), else at most two more
+    const long long span = (p.pair ? 2LL : 1LL) * part;
+    const long long nb_max = span % a->page_size == 0 ? span / a->page_size : span / a->page_size + 2;
     p.table_in_lanes = fast && nb_max <= kvbk::kLaneBlocks;
     const kvbk::Marks dm{mk.step.start ? mk.step.start : mk.decode.start, fused ? mk.step.stop : mk.decode.stop};
     const kvbk::Marks rm{mk.reduce.start, mk.step.stop ? mk.step.stop : mk.reduce.stop};
@@ -358,6 +368,13 @@ int kvb_set_stream(void* stream) {
     KVB_HIP(hipStreamWaitEvent(next, g.switch_ev, 0));
     g.stream = next;
     return KVB_OK;
+}
+
+int kvb_set_pair_mode(int mode) {
+    if (mode != KVB_PAIR_AUTO && mode != KVB_PAIR_OFF && mode != KVB_PAIR_ALWAYS) return -1;
+    const int prev = g.pair_mode;
+    g.pair_mode = mode;
+    return prev;
 }
 
 int kvb_synchronize(void) {
