@@ -426,6 +426,15 @@ static void load_row(const void* pool, int kv_type, size_t at, int D, float* dst
 }
 
 /* One partition of one (sequence, query head): the decode kernel's workgroup, one head of its group. */
+/* x rounded to fp16 and back (round to nearest even). */
+static inline float round_f16(float x) { return kvbo_f16_to_f32(kvbo_f32_to_f16(x)); }
+
+/* A signed byte digit of the int8 q split: rint(x) clamped to [-127, 127]. */
+static inline float digit_i8(float x) {
+    const float r = rintf(x);
+    return r < -127.0f ? -127.0f : r > 127.0f ? 127.0f : r;
+}
+
 static void model_partition(const split_job* j, int b, int h, int part) {
     const kvbo_shape* s = j->s;
     const int D = s->head_dim, P = j->page_size, Hkv = s->num_kv_heads;
@@ -438,10 +447,45 @@ static void model_partition(const split_job* j, int b, int h, int part) {
     const int32_t* bt = j->table + (size_t)b * j->max_blocks;
     float wm[kModelMaxWaves], wl[kModelMaxWaves], wacc[kModelMaxWaves][kModelMaxD];
     float krow[kModelMaxD], vrow[kModelTile][kModelMaxD], sc[kModelTile], vs[kModelTile];
+    /* q in the kernel's number formats (paged_decode_impl.hpp: the q split). q * scale is brought
+       below 2^14 (fp16) or 2^7 (int8) by a power of two `down`; the scores are multiplied back by
+       up = 1 / down. fp16: each element as a high and a low fp16 part (the MFMA's two columns of
+       the head). int8: three signed byte digits, x = d0 + d1 / 2^7 + d2 / 2^14 (the integer MFMA's
+       operands). fp32: q * scale as it is. */
+    float qhi[kModelMaxD], qlo[kModelMaxD], qd0[kModelMaxD], qd1[kModelMaxD], qd2[kModelMaxD];
+    float up = 1.0f, amax = 0.0f;
+    for (int d = 0; d < D; ++d) {
+        const float a = fabsf(qr[d] * j->scale);
+        amax = a > amax ? a : amax;
+    }
+    int e = 0;
+    if (j->kv_type != 0 && amax > 0.0f && amax <= FLT_MAX) {
+        frexpf(amax, &e); /* amax < 2^e */
+        e -= j->kv_type == 2 ? 7 : 14;
+    }
+    up = ldexpf(1.0f, e);
+    const float down = ldexpf(1.0f, -e);
+    for (int d = 0; d < D; ++d) {
+        const float x = qr[d] * j->scale * (j->kv_type == 0 ? 1.0f : down);
+        qhi[d] = j->kv_type == 1 ? round_f16(x) : x;
+        qlo[d] = j->kv_type == 1 ? round_f16(x - qhi[d]) : 0.0f;
+        qd0[d] = digit_i8(x);
+        const float r1 = (x - qd0[d]) * 128.0f;
+        qd1[d] = digit_i8(r1);
+        qd2[d] = digit_i8((r1 - qd1[d]) * 128.0f);
+    }
+    if (j->kv_type == 2 && !(amax <= FLT_MAX)) up = NAN; /* a non-finite q: its scores are NaN */
     for (int w = 0; w < j->waves; ++w) {
         float m = -INFINITY, l = 0.0f;
         float* acc = wacc[w];
-        for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+        /* p enters the P*V product as a high and a low fp16 part (fp16 and int8 caches), each with
+           its own accumulator column; int8: p * v_scale * 2^-ve, ve the exponent of the largest V
+           scale the wave has met, the accumulators rescaled when it grows and scaled by 2^ve at
+           the end. */
+        float acc_lo[kModelMaxD];
+        int ve = -160;
+        float vdown = 1.0f;
+        for (int d = 0; d < D; ++d) acc[d] = acc_lo[d] = 0.0f;
         for (int tt = t0 + w * kModelTile; tt < t1; tt += j->waves * kModelTile) {
             const int n = t1 - tt < kModelTile ? t1 - tt : kModelTile; /* tokens past t1 are masked */
             float mt = -INFINITY;
@@ -457,28 +501,65 @@ static void model_partition(const split_job* j, int b, int h, int part) {
                 load_row(j->v, j->kv_type, row, D, vrow[i]);
                 if (id < 0)
                     for (int d = 0; d < D; ++d) krow[d] = vrow[i][d] = 0.0f;
-                float dot = 0.0f;
-                for (int d = 0; d < D; ++d) dot += qr[d] * krow[d];
-                sc[i] = dot * j->scale;
-                vs[i] = 1.0f;
-                if (j->kv_type == 2) {
+                if (j->kv_type == 2) { /* exact integer dot products per digit, combined in fp32 */
+                    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
+                    for (int d = 0; d < D; ++d) {
+                        s0 += krow[d] * qd0[d];
+                        s1 += krow[d] * qd1[d];
+                        s2 += krow[d] * qd2[d];
+                    }
+                    sc[i] = (fmaf(s2, 1.0f / 16384.0f, s0) + s1 * (1.0f / 128.0f)) * up;
                     sc[i] *= j->k_scale[blk * Hkv + kvh];
                     vs[i] = j->v_scale[blk * Hkv + kvh];
+                } else { /* the high and the low column, summed */
+                    float shi = 0.0f, slo = 0.0f;
+                    for (int d = 0; d < D; ++d) {
+                        shi += krow[d] * qhi[d];
+                        slo += krow[d] * qlo[d];
+                    }
+                    sc[i] = (shi + slo) * up;
+                    vs[i] = 1.0f;
                 }
                 if (sc[i] > mt) mt = sc[i];
+            }
+            if (j->kv_type == 2) { /* the wave's V-scale exponent */
+                float vmx = 0.0f;
+                for (int i = 0; i < n; ++i) vmx = vs[i] > vmx ? vs[i] : vmx;
+                int ev = ve;
+                if (vmx > 0.0f) frexpf(vmx, &ev); /* vmx < 2^ev */
+                if (ev > ve) {
+                    const float nd = ldexpf(1.0f, -ev);
+                    const float resc = nd / vdown; /* a power of two: exact */
+                    for (int d = 0; d < D; ++d) {
+                        acc[d] *= resc;
+                        acc_lo[d] *= resc;
+                    }
+                    ve = ev;
+                    vdown = nd;
+                }
             }
             const float m_new = m > mt ? m : mt;
             const float corr = exp_ftz(m - m_new); /* rescales the tile-old state to the new max */
             l *= corr;
-            for (int d = 0; d < D; ++d) acc[d] *= corr;
+            for (int d = 0; d < D; ++d) {
+                acc[d] *= corr;
+                acc_lo[d] *= corr;
+            }
             for (int i = 0; i < n; ++i) {
                 const float p = exp_ftz(sc[i] - m_new);
                 l += p;
-                const float pv = p * vs[i];
-                for (int d = 0; d < D; ++d) acc[d] += pv * vrow[i][d];
+                const float pv = p * vs[i] * vdown;
+                const float phi = j->kv_type == 0 ? pv : round_f16(pv);
+                const float plo = j->kv_type == 0 ? 0.0f : round_f16(pv - phi);
+                for (int d = 0; d < D; ++d) {
+                    acc[d] += phi * vrow[i][d];
+                    acc_lo[d] += plo * vrow[i][d];
+                }
             }
             m = m_new;
         }
+        const float vupf = 1.0f / vdown; /* 2^ve (1 for fp32 and fp16) */
+        for (int d = 0; d < D; ++d) acc[d] = (acc[d] + acc_lo[d]) * vupf;
         wm[w] = m;
         wl[w] = l;
     }

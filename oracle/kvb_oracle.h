@@ -127,7 +127,10 @@ int kvbo_auto_part_tokens(int batch, int num_kv_heads, int max_len);
  * head) and partition of part_tokens tokens (src/kernels.metal:60-64): `waves` online-softmax
  * states over tiles of 16 tokens taken round robin (the tail tile masked at the sequence end), the
  * int8 K scale on the score and the V scale on p; the states merge with weights exp(m_w - M) into
- * the partition's (o / L, M, L) (src/kernels.metal:97-120). Then, as a second phase, the partition
+ * the partition's (o / L, M, L) (src/kernels.metal:97-120). The products use the kernel's number
+ * formats: q * scale scaled by a power of two, as high and low fp16 parts (fp16 caches) or three
+ * signed byte digits (int8), p (int8: p * v_scale, normalised by the wave's largest V-scale power
+ * of two) as high and low fp16 parts, each part with its own accumulator, summed at the end. Then, as a second phase, the partition
  * merge of paged_reduce (src/kernels.metal:124-147): out = sum w_i o_i / sum w_i with
  * w_i = l_i exp(m_i - M); an empty sequence gives 0. exp is evaluated as the GPU's exp unit
  * returns it, with results below 2^-126 zero.

@@ -8,10 +8,12 @@ caught when at least one test fails; the in-tree sources and builds are never to
 
 Groups:
   kernel  the reference's kernel mistakes (scripts/mutation.sh:50-59), its kernel-side boundary
-          mistakes (:33-36) and a few more, planted in the oracle's CPU model of this build's
-          split-K kernel (kvbo_split_decode in oracle/kvb_oracle.c). They are checked by
-          tests/test_split_model.py, which is the GPU parity battery (tests/parity_battery.py) run on
-          that model. No deliberately broken kernel runs on a GPU.
+          mistakes (:33-36) and mistakes in this build's arithmetic (the fp16 high/low split of q
+          and p, the int8 q digits, the V-scale normalisation), planted in the oracle's CPU model
+          of this build's split-K kernel (kvbo_split_decode in oracle/kvb_oracle.c, which uses the
+          kernel's number formats). They are checked by tests/test_split_model.py, which is the GPU
+          parity battery (tests/parity_battery.py) run on that model. No deliberately broken kernel
+          runs on a GPU (the GPU boxes forbid it), and the HIP kernel cannot run on the CPU.
   oracle  mistakes in the checker itself (fp64 attention, layout, quantiser, f16 rounding, RNG,
           storage-error bounds), checked by tests/test_oracle.py: the pins against the reference's
           own build, its golden vectors and closed forms.
@@ -77,8 +79,7 @@ MUTANTS = [
     K("no online-softmax rescale (corr = 1)",
       "const float corr = exp_ftz(m - m_new);", "const float corr = 1.0f;"),
     K("accumulator rounded to fp16 each step",
-      "for (int d = 0; d < D; ++d) acc[d] += pv * vrow[i][d];",
-      "for (int d = 0; d < D; ++d) acc[d] = kvbo_f16_to_f32(kvbo_f32_to_f16(acc[d] + pv * vrow[i][d]));"),
+      "acc[d] += phi * vrow[i][d];", "acc[d] = round_f16(acc[d] + phi * vrow[i][d]);"),
     K("off-by-one row inside a page",
       "const size_t row = ((blk * Hkv + kvh) * P + t % P) * D;",
       "const size_t row = ((blk * Hkv + kvh) * P + (t + 1) % P) * D;"),
@@ -102,7 +103,24 @@ MUTANTS = [
     K("partition merge has no case for an empty sequence", "if (parts == 0) {", "if (0) {"),
     K("query head served by the wrong KV head",
       "const int kvh = h / (s->num_heads / Hkv);", "const int kvh = h % Hkv;"),
-    K("softmax scale not applied", "sc[i] = dot * j->scale;", "sc[i] = dot;"),
+    K("softmax scale not applied",
+      "const float x = qr[d] * j->scale * (j->kv_type == 0 ? 1.0f : down);",
+      "const float x = qr[d] * (j->kv_type == 0 ? 1.0f : down);"),
+    # the kernel's number formats (paged_decode_impl.hpp: the q split, the score columns, the fp16
+    # split of p and the int8 V-scale normalisation), as the model restates them
+    K("fp16 q: low part dropped (q as one fp16 number)",
+      "qlo[d] = j->kv_type == 1 ? round_f16(x - qhi[d]) : 0.0f;", "qlo[d] = 0.0f;"),
+    K("scores: the power of two that scaled q not undone",
+      "sc[i] = (shi + slo) * up;", "sc[i] = shi + slo;"),
+    K("int8 q: third digit dropped", "qd2[d] = digit_i8((r1 - qd1[d]) * 128.0f);", "qd2[d] = 0.0f;"),
+    K("int8 q: second digit weighted 2^-6 instead of 2^-7",
+      "s1 * (1.0f / 128.0f)", "s1 * (1.0f / 64.0f)"),
+    K("int8 q: digits of q * scale unscaled (no per-head power of two)",
+      "e -= j->kv_type == 2 ? 7 : 14;", "e = j->kv_type == 2 ? 0 : e - 14;"),
+    K("p: low fp16 part dropped (p as one fp16 number)",
+      "const float plo = j->kv_type == 0 ? 0.0f : round_f16(pv - phi);", "const float plo = 0.0f;"),
+    K("int8: p * v_scale split into fp16 without the V-scale normalisation",
+      "const float nd = ldexpf(1.0f, -ev);", "const float nd = 1.0f;"),
     K("tail tile drops its last token",
       "const int n = t1 - tt < kModelTile ? t1 - tt : kModelTile;",
       "const int n = t1 - tt < kModelTile ? t1 - tt - 1 : kModelTile;"),

@@ -158,6 +158,24 @@ def check_huge_and_tiny_queries(kvb, oracle, run, kv="f16"):
         assert oracle.max_abs_diff(run(w, c, 64, True), want) <= tol, amp
 
 
+def check_huge_and_tiny_values(kvb, oracle, run, kv="i8"):
+    """K and V far from 1 in magnitude (1e-7, 1e3): int8 p * v_scale is normalised by the wave's
+    largest V-scale power of two before its fp16 split, which at 1e-7 would otherwise underflow;
+    fp16 stores the values as subnormals or near its range. Tolerance relative to max|v|."""
+    for amp in (1e-7, 1e3):
+        base = kvb.Workload(kvb.Shape(2, 8, 2, 128), kv, [300, 77], seed=61, varied=(kv == "i8"))
+        dt = base.k.dtype
+        k = (base.k.astype(np.float32) * amp).astype(dt)
+        v = (base.v.astype(np.float32) * amp).astype(dt)
+        w = kvb.Workload.from_arrays(kv, base.lens, base.q, k, v)
+        c = kvb.PagedCache(w, 16, 11, pool_factor=1.5, poison=True)
+        want, _ = expected(kvb, oracle, w, c)
+        vals = c.dequantized(w)[1] if kv == "i8" else w.v.astype(np.float32)
+        vmax = max(float(np.abs(vals[b, :, :L]).max()) for b, L in enumerate(w.lens) if L)
+        err = oracle.max_abs_diff(run(w, c, 64, True), want)
+        assert err <= 2e-5 * vmax, (amp, err, vmax)
+
+
 def check_storage_bound_f16(kvb, oracle, run):
     """c2's shape (8 x 4096 tokens, N(0,1)): the output against fp64 attention on the unrounded fp32
     data, within the derived fp16 storage bound (tests/gpu_tests.cpp:16-40)."""

@@ -91,6 +91,11 @@ def test_huge_and_tiny_queries(gpu, oracle, kv):
     pb.check_huge_and_tiny_queries(gpu, oracle, runner(gpu), kv)
 
 
+@pytest.mark.parametrize("kv", ["f16", "i8"])
+def test_huge_and_tiny_values(gpu, oracle, kv):
+    pb.check_huge_and_tiny_values(gpu, oracle, runner(gpu), kv)
+
+
 @pytest.mark.parametrize("kv", ["f32", "f16", "i8"])
 def test_ragged_batch_equals_each_sequence_alone(gpu, kv):
     """A ragged batch runs in the longest-first work order (grid y enumerates partitions, the

@@ -54,6 +54,11 @@ def test_huge_and_tiny_queries(kvb, oracle, model, kv):
     pb.check_huge_and_tiny_queries(kvb, oracle, model[0], kv)
 
 
+@pytest.mark.parametrize("kv", ["f16", "i8"])
+def test_huge_and_tiny_values(kvb, oracle, model, kv):
+    pb.check_huge_and_tiny_values(kvb, oracle, model[0], kv)
+
+
 def test_storage_bounds_c2_f16(kvb, oracle, model):
     pb.check_storage_bound_f16(kvb, oracle, model[0])
 
