@@ -12,12 +12,13 @@ the span of the stamps, percentiles of starts, loop durations and loop ends, the
 the loop, the merge time of the merging workgroups, and the time from the last loop end to the end.
 Median over 5 launches after 1 discarded. Prints a markdown table per configuration.
 
-With --where, also where the workgroups ran (wave 0's HW_ID and XCC_ID, stamped by the same build),
+With --warm, no flush before the launches (caches and the previous launch as a decode loop leaves
+them). With --where, also where the workgroups ran (wave 0's HW_ID and XCC_ID, stamped by the same build),
 for the last launch of each form: loop durations and loop ends per XCD, and per rank of a workgroup
 among those that ran on the same CU (by start time), which separates a CU's first workgroup from the
 ones that shared or followed it.
 
-usage: python3 kv-cache-bench_amd/bench/wg_timeline.py [--where] c2 [c3 c4 c5i8 ...]
+usage: python3 kv-cache-bench_amd/bench/wg_timeline.py [--where] [--warm] c2 [c3 c4 c5i8 ...]
 """
 from __future__ import annotations
 
@@ -72,12 +73,13 @@ def where_tables(t, start, loop_end):
     return lines
 
 
-def summarise(kvb, dev, part, mode, read, reps=6, where=None):
+def summarise(kvb, dev, part, mode, read, reps=6, where=None, warm=False):
     buf = np.zeros(GROUPS * WORDS, np.uint64)
     prev = 0
     rows = []
     for rep in range(reps):
-        kvb.flush_gpu_caches()
+        if not warm:
+            kvb.flush_gpu_caches()
         if mode == "fused":
             ms = dev.run(part)
         elif mode == "decode":
@@ -117,7 +119,8 @@ def summarise(kvb, dev, part, mode, read, reps=6, where=None):
 
 def main(args):
     show_where = "--where" in args
-    configs = [a for a in args if a != "--where"] or ["c2"]
+    warm = "--warm" in args
+    configs = [a for a in args if a not in ("--where", "--warm")] or ["c2"]
     kvb = graft.load_package()
     if not kvb.gpu_available():
         sys.exit("wg_timeline: no GPU")
@@ -134,7 +137,7 @@ def main(args):
         wheres = {}
         for mode in ("fused", "decode", "loads"):
             wheres[mode] = []
-            r = summarise(kvb, dev, part, mode, read, where=wheres[mode] if show_where else None)
+            r = summarise(kvb, dev, part, mode, read, where=wheres[mode] if show_where else None, warm=warm)
             cells = [f"{r[k]:.0f}" if k in ("wgs", "mergers") else f"{r[k]:.2f}" for k, _ in COLUMNS]
             print(f"| {mode} | " + " | ".join(cells) + " |", flush=True)
         print()
