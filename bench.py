@@ -72,6 +72,17 @@ def warm_chain(kvb, dev, part, steps=20):
     return dev.run(part, steps=steps) / steps
 
 
+def graph_chain(kvb, dev, part, steps=20, launches=5):
+    """Warm back-to-back steps replayed from a captured HIP graph (kvb_graph_capture_paged): the
+    steps of a serving loop with one launch per `steps`; per-step time, median over launches."""
+    graph = dev.capture_graph(part, steps)
+    try:
+        graph.launch()
+        return statistics.median(graph.launch() for _ in range(launches)) / steps
+    finally:
+        graph.free()
+
+
 def warm_steps(kvb, dev, part, steps=30):
     """Single steps with no flush between them (one launch and event pair each, waited for): beside
     the cold steps, what the flush changes."""
@@ -255,6 +266,7 @@ def main():
         if c.page_size % 16 == 0 and part_res % 16 == 0:
             extras["loads_only_us"] = round(loads_only(kvb, dev, part) * 1e3, 2)
         extras["warm_chain_us"] = round(warm_chain(kvb, dev, part) * 1e3, 2)
+        extras["graph_chain_us"] = round(graph_chain(kvb, dev, part) * 1e3, 2)
         extras["warm_gbps"] = round(bytes_step / (extras["warm_chain_us"] * 1e-6) / 1e9, 1)
         extras["warm_step_us"] = round(warm_steps(kvb, dev, part) * 1e3, 2)
         extras["empty_step_us"] = round(empty_steps(kvb, w, part) * 1e3, 2)

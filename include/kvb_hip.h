@@ -133,6 +133,21 @@ int kvb_run_paged_noalloc(const kvb_paged_args* a);
 /* `steps` decode steps on the same inputs, back to back on one stream, one event pair around them
  * (run_paged_steps, src/metal_attn.hpp:91). */
 int kvb_run_paged_steps(const kvb_paged_args* a, int steps, double* ms);
+/* No counterpart in the reference (its steps are Metal command buffers): kvb_run_paged_steps' `steps`
+ * decode steps captured once into a HIP graph, for serving loops that replay a fixed step with one
+ * launch. The graph owns its split-K workspace and merge counters (allocated and zeroed here, before
+ * the capture, and freed by kvb_graph_destroy), so no later call can move them; it holds the
+ * caller's pointers from `a` (q, k, v, tables, lengths, scales, out), which must stay valid and keep
+ * their shapes while it exists. The captured steps are the same kernels, in the same order, as
+ * kvb_run_paged_steps: the same bits. They allocate nothing and contain no memset node. Same
+ * refusals as kvb_run_paged, plus KVB_EINVAL for steps < 1, a->workspace set, or pipelined mode.
+ * *graph receives an opaque handle. */
+int kvb_graph_capture_paged(const kvb_paged_args* a, int steps, void** graph);
+/* Launches a captured graph on the library's current stream. *ms = GPU time of the launch (hipEvent
+ * pair); 0 in pipelined mode. KVB_EINVAL for a null handle. */
+int kvb_graph_launch(void* graph, double* ms);
+/* Waits for the library's stream, then frees the graph and its workspace. Null is a no-op. */
+int kvb_graph_destroy(void* graph);
 /* One synchronous decode step in the reference's two-kernel form, timed per kernel: *decode_ms and
  * *reduce_ms are the hipEvent times of paged_decode (no merge) and of paged_reduce. Not in the
  * reference (its timing is per command buffer, src/metal_attn.mm:119-130). */

@@ -88,6 +88,9 @@ _SIGS = {
     "kvb_check_paged": ([_PA], _i),
     "kvb_run_paged": ([_PA, _d], _i),
     "kvb_run_paged_steps": ([_PA, _i, _d], _i),
+    "kvb_graph_capture_paged": ([_PA, _i, ctypes.POINTER(ctypes.c_void_p)], _i),
+    "kvb_graph_launch": ([ctypes.c_void_p, _d], _i),
+    "kvb_graph_destroy": ([ctypes.c_void_p], _i),
     "kvb_run_paged_split": ([_PA, _d, _d], _i),
     "kvb_run_paged_loads": ([_PA, _d], _i),
     "kvb_set_pair_mode": ([_i], _i),
@@ -408,6 +411,14 @@ class DeviceCase:
         check(hip.kvb_run_paged_split(ctypes.byref(a), ctypes.byref(d), ctypes.byref(r)), "run_paged_split")
         return d.value, r.value
 
+    def capture_graph(self, part_tokens=0, steps=1) -> "PagedGraph":
+        """`steps` decode steps captured into a HIP graph (kvb_graph_capture_paged), with its own
+        workspace; launch() replays them. Keep this case alive while the graph is."""
+        h = ctypes.c_void_p()
+        a = self.args(part_tokens)
+        check(hip.kvb_graph_capture_paged(ctypes.byref(a), steps, ctypes.byref(h)), "graph_capture_paged")
+        return PagedGraph(h)
+
     def run_loads(self, part_tokens=0):
         """The decode's loads alone (kvb_run_paged_loads): GPU ms of paged_decode's memory traffic
         with no arithmetic; the output is not written."""
@@ -432,6 +443,24 @@ class DeviceCase:
         for b in (self.q, self.k, self.v, self.table, self.lens, self.k_scale, self.v_scale, self.out):
             if b is not None:
                 b.free()
+
+
+class PagedGraph:
+    """A captured decode loop (kvb_graph_capture_paged): launch() replays it on the library's stream
+    and returns its GPU ms (0 in pipelined mode); free() releases it and its workspace."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    def launch(self) -> float:
+        ms = ctypes.c_double()
+        check(hip.kvb_graph_launch(self.handle, ctypes.byref(ms)), "graph_launch")
+        return ms.value
+
+    def free(self):
+        if self.handle:
+            check(hip.kvb_graph_destroy(self.handle), "graph_destroy")
+            self.handle = None
 
 
 def run_attention_fp64(w: Workload, out: Buffer, q: Buffer, k: Buffer, v: Buffer, lens: Buffer) -> float:

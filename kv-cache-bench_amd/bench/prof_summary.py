@@ -108,6 +108,7 @@ def main(cfg, out):
     keys = [("us_per_step", "step, cold (median of 30)"), ("unfused_decode_us", "paged_decode alone, two-kernel form"),
             ("unfused_reduce_us", "paged_reduce, two-kernel form"), ("loads_only_us", "the decode's loads alone"),
             ("warm_step_us", "step, warm (no flush, one launch each)"), ("warm_chain_us", "step, warm chain of 20"),
+            ("graph_chain_us", "step, warm, 20 replayed from one HIP graph"),
             ("empty_step_us", "the same launch with every sequence empty"),
             ("int8_us_per_step", "c4's shape with an int8 cache"), ("int8_loads_only_us", "its loads alone")]
     print("| measurement | us |")

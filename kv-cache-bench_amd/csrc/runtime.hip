@@ -468,6 +468,94 @@ int kvb_run_paged_steps(const kvb_paged_args* a, int steps, double* ms) {
 
 int kvb_run_paged(const kvb_paged_args* a, double* ms) { return kvb_run_paged_steps(a, 1, ms); }
 
+// A captured decode loop: the executable graph and the workspace it writes.
+struct PagedGraph {
+    hipGraphExec_t exec = nullptr;
+    void* ws = nullptr;        // [split-K workspace][counters]
+};
+
+int kvb_graph_capture_paged(const kvb_paged_args* a, int steps, void** graph) {
+    if (!graph) return fail(KVB_EINVAL, "null graph handle pointer");
+    *graph = nullptr;
+    if (int st = validate_paged(a)) return st;
+    if (steps < 1) return fail(KVB_EINVAL, "kvb_graph_capture_paged: steps < 1");
+    if (a->workspace) return fail(KVB_EINVAL, "kvb_graph_capture_paged takes no workspace: the graph owns its own");
+    if (int st = ensure_device()) return st;
+    if (g.pipelined) return fail(KVB_EINVAL, "kvb_graph_capture_paged: not in pipelined mode");
+    // The graph's own workspace and counters, zeroed by a fill kernel before the capture (each fused
+    // launch leaves the counters at 0 again, so every replay starts from zeros).
+    const size_t ws_bytes = (workspace_need(a) + 255) / 256 * 256;
+    const size_t cnt_bytes = ((size_t)a->batch * a->num_heads * sizeof(int) + 255) / 256 * 256;
+    auto* pg = new PagedGraph;
+    auto cleanup = [&](int st) {
+        if (pg->ws) (void)hipFree(pg->ws);
+        delete pg;
+        return st;
+    };
+    if (hipMalloc(&pg->ws, ws_bytes + cnt_bytes) != hipSuccess)
+        return cleanup(fail(KVB_ERUNTIME, "kvb_graph_capture_paged: workspace allocation failed"));
+    char* base = static_cast<char*>(pg->ws);
+    int* counters = reinterpret_cast<int*>(base + ws_bytes);
+    if (hipError_t e = kvbk::launch_fill(counters, cnt_bytes / 16, 0u, g.stream); e != hipSuccess)
+        return cleanup(fail(KVB_ERUNTIME, std::string("graph counter fill: ") + hipGetErrorString(e)));
+    if (hipStreamSynchronize(g.stream) != hipSuccess)
+        return cleanup(fail(KVB_ERUNTIME, "kvb_graph_capture_paged: stream synchronize failed"));
+    const size_t slots = (size_t)a->batch * a->num_heads * (size_t)max_parts_of(a);
+    float* part_out = reinterpret_cast<float*>(base);
+    float2* part_ml = reinterpret_cast<float2*>(base + slots * (size_t)a->head_dim * sizeof(float));
+    if (a->batch == 0) {  // nothing to capture: an empty graph
+        hipGraph_t empty = nullptr;
+        if (hipGraphCreate(&empty, 0) != hipSuccess ||
+            hipGraphInstantiate(&pg->exec, empty, nullptr, nullptr, 0) != hipSuccess) {
+            if (empty) (void)hipGraphDestroy(empty);
+            return cleanup(fail(KVB_ERUNTIME, "kvb_graph_capture_paged: empty graph"));
+        }
+        (void)hipGraphDestroy(empty);
+        *graph = pg;
+        return KVB_OK;
+    }
+    hipGraph_t captured = nullptr;
+    if (hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
+        return cleanup(fail(KVB_ERUNTIME, "kvb_graph_capture_paged: hipStreamBeginCapture failed"));
+    int st = KVB_OK;
+    for (int i = 0; i < steps && st == KVB_OK; ++i) st = enqueue_paged(a, part_out, part_ml, true, StepMarks{}, false, counters);
+    const hipError_t ce = hipStreamEndCapture(g.stream, &captured);
+    if (st != KVB_OK || ce != hipSuccess) {
+        if (captured) (void)hipGraphDestroy(captured);
+        return cleanup(st != KVB_OK ? st : fail(KVB_ERUNTIME, std::string("hipStreamEndCapture: ") + hipGetErrorString(ce)));
+    }
+    const hipError_t ie = hipGraphInstantiate(&pg->exec, captured, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(captured);
+    if (ie != hipSuccess) return cleanup(fail(KVB_ERUNTIME, std::string("hipGraphInstantiate: ") + hipGetErrorString(ie)));
+    *graph = pg;
+    return KVB_OK;
+}
+
+int kvb_graph_launch(void* graph, double* ms) {
+    if (ms) *ms = 0.0;
+    if (!graph) return fail(KVB_EINVAL, "null graph");
+    if (int st = ensure_device()) return st;
+    auto* pg = static_cast<PagedGraph*>(graph);
+    hipEvent_t e0, e1;
+    if (int st = get_event(&e0)) return st;
+    if (int st = get_event(&e1)) return st;
+    KVB_HIP(hipEventRecord(e0, g.stream));
+    KVB_HIP(hipGraphLaunch(pg->exec, g.stream));
+    KVB_HIP(hipEventRecord(e1, g.stream));
+    return finish(e0, e1, ms);
+}
+
+int kvb_graph_destroy(void* graph) {
+    if (!graph) return KVB_OK;
+    if (int st = ensure_device()) return st;
+    auto* pg = static_cast<PagedGraph*>(graph);
+    KVB_HIP(hipStreamSynchronize(g.stream));
+    if (pg->exec) KVB_HIP(hipGraphExecDestroy(pg->exec));
+    if (pg->ws) KVB_HIP(hipFree(pg->ws));
+    delete pg;
+    return KVB_OK;
+}
+
 // kvb_run_paged's step with the workspace and counters in `scratch` (no allocation, no events, no
 // wait). The fused merge needs B * H / qg counters, qg the query heads per workgroup, at most B * H.
 int kvb_run_paged_noalloc(const kvb_paged_args* a) {
