@@ -148,6 +148,24 @@ double run_attention_fp64(const NaiveArgs&);
 // `steps` decode steps on the same inputs, back to back on one stream (src/metal_attn.hpp:89-91).
 double run_paged_steps(const PagedArgs&, int steps);
 
+// `steps` decode steps captured into a HIP graph (kvb_graph_capture_paged; not in the reference,
+// whose steps are command buffers), for loops that replay a fixed step with one launch. launch()
+// replays them on the library's stream and returns their GPU milliseconds (0 in pipelined mode).
+// The graph owns its workspace and keeps the buffers of its PagedArgs by address: keep them alive,
+// and their shapes unchanged, while it exists. Throws as run_paged does.
+class PagedGraph {
+public:
+    PagedGraph(const PagedArgs&, int steps);
+    ~PagedGraph();
+    PagedGraph(const PagedGraph&) = delete;
+    PagedGraph& operator=(const PagedGraph&) = delete;
+    double launch();
+
+private:
+    const PagedArgs* args_;
+    void* handle_ = nullptr;
+};
+
 // One decode step with the GPU time of each kernel.
 struct KernelTimes {
     double decode_ms = 0, reduce_ms = 0;

@@ -45,6 +45,7 @@ struct Options {
     std::vector<int> lens{512, 1024, 2048, 4096, 8192, 16384, 32768}, pages{16, 32, 64, 128}, parts{0};
     std::vector<KvType> types{KvType::f32, KvType::f16, KvType::i8};
     int reps = 30, warmup = 3, cpu_reps = 3, chain = 0;
+    bool graph = false;  // --graph: the chain's paged rows also replayed from a captured HIP graph
     bool naive = true, cpu = true, flush = true, per_head = false, bw = false, sync = false, accuracy = false,
          loads = false, schema = false;
     std::string dump, config, cpu_ref;
@@ -84,6 +85,7 @@ const std::vector<Flag>& flags() {
         {"--warmup", true, [](Options& o, const char* v) { o.warmup = std::atoi(v); }},
         {"--cpu-reps", true, [](Options& o, const char* v) { o.cpu_reps = std::atoi(v); }},
         {"--chain", true, [](Options& o, const char* v) { o.chain = std::atoi(v); }},
+        {"--graph", false, [](Options& o, const char*) { o.graph = true; }},
         {"--dump", true, [](Options& o, const char* v) { o.dump = v; }},
         {"--types", true,
          [](Options& o, const char* v) {
@@ -397,7 +399,8 @@ int mode_dump(const Options& o) {
 }
 
 // --chain=N: N warm decode steps in one submission (run_paged_steps), wall clock until they complete
-// divided by N, for the contiguous layout (one block per sequence) and the paged one (page 16).
+// divided by N, for the contiguous layout (one block per sequence) and the paged one (page 16). With
+// --graph, the paged chain is also captured once into a HIP graph and replayed (impl ours-graph).
 // max_err is against fp64 on the stored values (f32/f16) or the unquantised data (i8).
 int mode_chain(const Options& o) {
     const Table t(kChainSchema);
@@ -418,24 +421,39 @@ int mode_chain(const Options& o) {
                     const double ms = std::chrono::duration<double, std::milli>(Clock::now() - t0).count();
                     if (i >= o.warmup) wall.push_back(ms / o.chain), gpu.push_back(g / o.chain);
                 }
-                const Sample s = summarise(wall);
                 const double bytes = double(cache.bytes()) + double(w.out_floats()) * 2 * sizeof(float);
-                t.row()
-                    .text("impl", "ours")
-                    .text("layout", contiguous ? "contiguous" : "paged16")
-                    .text("dtype", name(type))
-                    .count("batch", w.shape.batch)
-                    .count("seq_len", L)
-                    .count("chain", o.chain)
-                    .count("reps", o.reps)
-                    .fixed("median_us", s.median_us(), 2)
-                    .fixed("min_us", s.min * 1e3, 2)
-                    .fixed("max_us", s.max * 1e3, 2)
-                    .fixed("gbps", gbps(bytes, s), 1)
-                    .general("max_err", err)
-                    .text("err_vs", type == KvType::i8 ? "fp32_data" : "stored")
-                    .fixed("gpu_us", summarise(gpu).median_us(), 2)
-                    .emit();
+                auto emit = [&](const char* impl, const std::vector<double>& wl, const std::vector<double>& gp,
+                                double e) {
+                    const Sample s = summarise(wl);
+                    t.row()
+                        .text("impl", impl)
+                        .text("layout", contiguous ? "contiguous" : "paged16")
+                        .text("dtype", name(type))
+                        .count("batch", w.shape.batch)
+                        .count("seq_len", L)
+                        .count("chain", o.chain)
+                        .count("reps", o.reps)
+                        .fixed("median_us", s.median_us(), 2)
+                        .fixed("min_us", s.min * 1e3, 2)
+                        .fixed("max_us", s.max * 1e3, 2)
+                        .fixed("gbps", gbps(bytes, s), 1)
+                        .general("max_err", e)
+                        .text("err_vs", type == KvType::i8 ? "fp32_data" : "stored")
+                        .fixed("gpu_us", summarise(gp).median_us(), 2)
+                        .emit();
+                };
+                emit("ours", wall, gpu, err);
+                if (o.graph && !contiguous) {  // the same chain, captured once and replayed
+                    PagedGraph graph(args, o.chain);
+                    std::vector<double> gwall, ggpu;
+                    for (int i = 0; i < o.warmup + o.reps; ++i) {
+                        const auto t0 = Clock::now();
+                        const double g = graph.launch();
+                        const double ms = std::chrono::duration<double, std::milli>(Clock::now() - t0).count();
+                        if (i >= o.warmup) gwall.push_back(ms / o.chain), ggpu.push_back(g / o.chain);
+                    }
+                    emit("ours-graph", gwall, ggpu, max_abs_diff(out.as<float>(), ref.data(), ref.size()));
+                }
             }
         }
     return 0;

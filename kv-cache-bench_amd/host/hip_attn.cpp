@@ -156,6 +156,22 @@ double run_paged_steps(const PagedArgs& a, int steps) {
 
 double run_paged(const PagedArgs& a) { return run_paged_steps(a, 1); }
 
+PagedGraph::PagedGraph(const PagedArgs& a, int steps) : args_(&a) {
+    kvb_paged_args c = view(a);
+    check(kvb_check_paged(&c), "capture_paged_graph");
+    upload_inputs(a);
+    check(kvb_graph_capture_paged(&c, steps, &handle_), "capture_paged_graph");
+}
+
+PagedGraph::~PagedGraph() { (void)kvb_graph_destroy(handle_); }
+
+double PagedGraph::launch() {
+    double ms = 0;
+    check(kvb_graph_launch(handle_, &ms), "graph_launch");
+    mark_written(*args_);
+    return ms;
+}
+
 KernelTimes run_paged_split(const PagedArgs& a) {
     kvb_paged_args c = view(a);
     check(kvb_check_paged(&c), "run_paged_split");

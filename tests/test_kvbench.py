@@ -147,6 +147,27 @@ def test_kvbench_chain(gpu):
 
 
 @pytest.mark.gpu
+def test_kvbench_chain_graph(gpu):
+    """--chain=N --graph: each paged16 chain is also captured into a HIP graph and replayed (impl
+    ours-graph), with the same schema and the same error as the eager chain's row."""
+    out = subprocess.run([KVBENCH, "--chain=8", "--graph", "--batch=2", "--lens=1000", "--reps=3", "--warmup=1",
+                          "--types=f16,i8"], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    head, rows = csv_rows(out.stdout)
+    ref, own = REFERENCE_HEADERS["chain"]
+    assert ",".join(head) == ref + "," + own
+    eager = {r["dtype"]: r for r in rows if r["impl"] == "ours" and r["layout"] == "paged16"}
+    graph = {r["dtype"]: r for r in rows if r["impl"] == "ours-graph"}
+    assert set(graph) == set(eager) == {"f16", "i8"}
+    for t, r in graph.items():
+        assert r["layout"] == "paged16" and r["chain"] == "8"
+        assert r["max_err"] == eager[t]["max_err"], (t, r["max_err"], eager[t]["max_err"])
+        assert float(r["median_us"]) > 0 and float(r["gpu_us"]) > 0
+    progress(f"[kvbench] chain of 8, f16 paged16: eager {eager['f16']['gpu_us']} us, graph {graph['f16']['gpu_us']} us "
+             "per step")
+
+
+@pytest.mark.gpu
 def test_reference_bench_runs_on_the_drop_in(gpu):
     """The reference's own bench/bench.cpp, compiled unmodified against this build's headers
     (oracle/_ref/kvbench): its sweep runs on MI355X, with its CPU rows from its own kvref, and the
