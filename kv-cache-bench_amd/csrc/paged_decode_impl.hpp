@@ -331,9 +331,9 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     constexpr int NJ = T::NJ, VL = T::VL, NV = T::NV, NMB = D / 16;
     constexpr bool F32 = KIND == KV_F32;
     static_assert(QG == 1 || QG == 2 || QG == 4 || QG == 8, "QG must be 1, 2, 4 or 8");
-    // Tile register buffers per wave: one computed, NBUF - 1 in flight. fp32 tiles are too large
-    // for more than one. (Three for int8, whose tiles are half an fp16 tile, spill at head_dim 128
-    // and measured slower.)
+    // Tile register buffers per wave: one computed while the next is loaded (see the tile walk).
+    // fp32 tiles are too large for more than one. (Three for int8, whose tiles are half an fp16
+    // tile, spill at head_dim 128 and measured slower.)
     constexpr int NBUF = F32 ? 1 : 2;
 
     // Per wave: the V tile (32 rows of D elements, swizzled); after the loop it holds the wave's
@@ -779,15 +779,18 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    // ---- walk the tiles, NBUF - 1 tiles in flight while one is computed: buffer k holds the
-    // wave's tiles k, k + NBUF, ... The prefetch is unconditional (past the end it reads zeros) so
-    // no branch splits the load counters the compiler tracks. The loop runs whole rounds of NBUF
-    // steps and has one exit: with an exit inside a round, the loop head is also reached from
-    // mid-round paths, where fewer loads are in flight, and its wait for buffer 0 then drains the
-    // later buffers too. The last round may step past the wave's last tile: such a step masks every
+    // ---- walk the tiles: buffer k holds the wave's tiles k, k + NBUF, ... Each step first waits
+    // until the tile it computes has arrived (the only loads outstanding), then issues the next
+    // tile's loads, then computes: one tile in flight per wave at any time, its latency under the
+    // computation. Issuing the next tile before that wait instead (two in flight while waiting)
+    // kept more bytes in flight per CU and was slower: on MI355X boxes where c4 ran 85.4-86.7 us
+    // that way it ran 83.8-84.0 us this way, and c5 fp16 330-332 against 338 us; elsewhere the two
+    // were within noise. The prefetch is unconditional (past the end it reads zeros) so no branch
+    // splits the load counters the compiler tracks. The loop runs whole rounds of NBUF steps and
+    // has one exit. The last round may step past the wave's last tile: such a step masks every
     // score (p = 0, corr = 1 exactly), reads zeros or masked rows, and at most renormalises the
     // int8 accumulators by a power of two, so it changes nothing. (sched_barrier: the scheduler
-    // would otherwise sink part of the prefetch below the wait for the tile being computed.)
+    // would otherwise move part of the prefetch across the wait or below the computation.)
     // ---- the wave's state -> LDS: [QG][D] fp32 (a high-column lane (hl == 0) holds d = 16 mb +
     // 4 q4 + i (i < 4) of head hh, one 16-byte chunk per mb; chunk c of head h's row is stored at
     // c ^ (h & 7) so that the 8 heads' rows do not all start in the same LDS banks) and (m, l).
@@ -816,6 +819,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     for (int rd = 0; rd < rounds; ++rd) {
 #pragma unroll
         for (int k = 0; k < NBUF; ++k) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // tile `it` (buffer k) has arrived
             load_tile(r[(k + NBUF - 1) % NBUF], t0 + (it + (NBUF - 1) * W) * kTok);
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (PAIR && !LOADS) {
