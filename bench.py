@@ -251,10 +251,11 @@ def main():
     log(f"{args.config}: step median {med * 1e3:.1f} us (mean {kernel_avg * 1e3:.1f} us), {value:.0f} GB/s; "
         f"wall {wall:.3f}s for {args.steps} steps")
 
-    traffic = None
+    traffic = tcc_hit = None
     if args.config == "c4" and os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+            rec = json.load(f)
+        traffic, tcc_hit = rec.get("bytes_per_launch"), rec.get("tcc_hit_rate")
 
     extras = {}
     if w.kv_type == kvb.KV_I8:
@@ -322,6 +323,7 @@ def main():
                    "kv_storage": storage, "bytes_per_step": bytes_step, "timed_wall_s": round(wall, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "tcc_hit_rate": tcc_hit,
                      "kernel": "paged_decode", "kernel_avg_us": round(kernel_avg * 1e3, 2),
                      "bytes_per_launch": bytes_step},
         "cpu_baseline": cpu,

@@ -78,6 +78,16 @@ def main(cfg, out):
     fetch_kib, write_kib = statistics.mean(f_dec), statistics.mean(w_dec)
     traffic = fetch_kib * 1024 * f_factor + write_kib * 1024 * w_factor
 
+    tcc = counter_rows(out, "tcc")
+    t_dec = [c for k, c in tcc if k == "decode"][-10:]
+    t_read = [c for k, c in tcc if k == "read"]
+
+    def hit_rate(rows):
+        hit = sum(c["TCC_HIT_sum"] for c in rows)
+        return hit / (hit + sum(c["TCC_MISS_sum"] for c in rows))
+
+    dec_hit, read_hit = hit_rate(t_dec), hit_rate(t_read)
+
     sq = [c for k, c in counter_rows(out, "sq") if k == "decode"][-10:]
     sq_names = sorted(sq[0])
     waves = statistics.mean(c["SQ_WAVES"] for c in sq)
@@ -94,7 +104,7 @@ def main(cfg, out):
     print("That script runs, from /tmp with TMPDIR=/tmp (R = the repository root):\n")
     print("```")
     print(f"python3 $R/bench.py --no-cpu --config {cfg}")
-    for what in ("--kernel-trace --stats", "--pmc FETCH_SIZE", "--pmc WRITE_SIZE",
+    for what in ("--kernel-trace --stats", "--pmc FETCH_SIZE", "--pmc WRITE_SIZE", "--pmc TCC_HIT_sum TCC_MISS_sum",
                  "--pmc SQ_WAVES SQ_INSTS_VALU SQ_INSTS_LDS SQ_INSTS_SALU SQ_INSTS_VMEM_RD SQ_WAVE_CYCLES "
                  "SQ_BUSY_CYCLES SQ_WAIT_INST_ANY GRBM_GUI_ACTIVE"):
         n = 30 if "trace" in what else 10
@@ -138,6 +148,21 @@ def main(cfg, out):
     print("|---|---|---|---|---|")
     print(f"| {fetch_kib:.0f} | {write_kib:.0f} | {traffic:.0f} | {algo:.0f} | {traffic / algo:.4f} |\n")
 
+    print("## L2 (TCC) hit rate (TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum), the 10 timed dispatches)\n")
+    print("Every K/V byte is read once per step, so the decode's hits are requests for a line that an earlier "
+          "request already brought in. One K load instruction reads 16 bytes per lane for 16 tokens (the MFMA "
+          "operand layout): 64 bytes of each of 16 rows at fp16 and int8, so each 128-byte K line is two "
+          "requests and the second hits. One V load instruction reads whole rows, a request per line. K and V "
+          "are half the lines each, which gives one hit per two misses: a rate of 1/3. Misses equal the lines "
+          "read (algorithmic bytes / 128). The 1 GiB flush read in the same run is a plain streaming read for "
+          "comparison.\n")
+    print("| kernel | TCC_HIT_sum | TCC_MISS_sum | hit rate |")
+    print("|---|---|---|---|")
+    for what, rows, rate in (("paged_decode", t_dec, dec_hit), ("read_bw, 1 GiB flush", t_read, read_hit)):
+        print(f"| {what} | {statistics.mean(c['TCC_HIT_sum'] for c in rows):.0f} | "
+              f"{statistics.mean(c['TCC_MISS_sum'] for c in rows):.0f} | {rate:.4f} |")
+    print()
+
     print("## SQ counters, paged_decode (mean per timed dispatch, and per wave)\n")
     print("SQ_WAVE_CYCLES, SQ_BUSY_CYCLES and SQ_WAIT_INST_ANY count in units of 4 cycles; GRBM_GUI_ACTIVE is "
           "the value rocprofv3 reports for the dispatch.\n")
@@ -154,7 +179,8 @@ def main(cfg, out):
         with open(os.path.join(out, "traffic.json"), "w") as f:
             json.dump({"kernel": f"paged_decode f16 c4 (fused): {kname}", "bytes_per_launch": round(traffic),
                        "fetch_kib": fetch_kib, "write_kib": write_kib, "fetch_factor": f_factor,
-                       "write_factor": w_factor, "source": "paged_decode_c4.md"}, f, indent=1)
+                       "write_factor": w_factor, "tcc_hit_rate": round(dec_hit, 4),
+                       "source": "paged_decode_c4.md"}, f, indent=1)
 
 
 if __name__ == "__main__":
