@@ -70,7 +70,7 @@ inline int auto_part_tokens(const Shape& s, int max_len) {
 
 // The MI355X partition policy: the largest power of two in [min_part, max_part] whose workgroup
 // count B * ceil(H / qg) * ceil(max_len / part) still reaches `min_groups` (qg: the query heads one
-// workgroup serves). Longer partitions mean fewer partial results to merge and a shorter prologue
+// workgroup serves, kvb_heads_per_workgroup). Longer partitions mean fewer partial results to merge and a shorter prologue
 // per token; enough workgroups keep enough bytes in flight. Measured on MI355X (c4): fastest at
 // one workgroup per CU (min_groups 256, the default).
 int mi355x_part_tokens(const Shape& s, int max_len, int min_groups = 256, int min_part = 256, int max_part = 4096);

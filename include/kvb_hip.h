@@ -99,6 +99,13 @@ int kvb_auto_part_tokens(int batch, int num_kv_heads, int max_len);
 int kvb_paged_max_parts(const kvb_paged_args* a);
 /* Bytes of the workspace a call with these arguments uses (0 on bad arguments). */
 size_t kvb_paged_workspace_bytes(const kvb_paged_args* a);
+/* Query heads one paged_decode workgroup serves, which read each K/V page once together: with
+ * share_kv, the largest divisor of the group num_heads / num_kv_heads that is at most 8 (a group
+ * of 7 is one workgroup per KV head, a group of 12 two of 6, a group of 16 two of 8), else 1.
+ * The reference's kernel serves the whole group from one threadgroup (QG = GROUP,
+ * src/metal_attn.mm:64-80); here a workgroup's score MFMA holds at most 8 heads. Returns -1 on
+ * bad arguments (num_kv_heads <= 0, num_heads not a positive multiple of it). */
+int kvb_heads_per_workgroup(int num_heads, int num_kv_heads, int share_kv);
 
 /* The refusals of kvb_run_paged alone (KVB_OK or KVB_EINVAL): reads only host_seq_lens and the
  * sizes, needs no GPU. Lets a host layer refuse before it uploads anything. */

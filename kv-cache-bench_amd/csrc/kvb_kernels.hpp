@@ -91,6 +91,10 @@ struct DecodeParams {
     // multiple of 2 * kTile * decode_waves(kind) (32-token tiles, dealt round robin to the waves), so
     // that each partition keeps its tiles' waves and order.
     int pair;
+    // Query heads per workgroup: a divisor of group, at most the kernel's QG; read by the PART
+    // kernels only (the others serve QG heads). Last, so that it leaves the other fields' offsets
+    // in the kernel arguments as they were.
+    int qg;
 };
 
 // Blocks of one partition that paged_decode holds in lanes: one per lane of one VGPR (and, for int8,
@@ -164,7 +168,8 @@ inline void launch_marked(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipSt
 }
 
 // paged_decode for one storage kind: grid (H / qg, batch, max_parts), or (H / qg, ragged_items, 1)
-// for a ragged batch, decode_waves(kind) waves per workgroup. `fast`: every 16-token tile lies inside one page (page_size % 16 == 0 and
+// for a ragged batch, decode_waves(kind) waves per workgroup. qg (= p.qg, 1 to 8) picks the kernel
+// built for the next of 1, 2, 4 and 8 query heads; its columns past qg are idle. `fast`: every 16-token tile lies inside one page (page_size % 16 == 0 and
 // part_tokens % 16 == 0), so block ids and scales are read once per tile.
 hipError_t launch_paged_decode_f32(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s,
                                    const Marks& m = {});

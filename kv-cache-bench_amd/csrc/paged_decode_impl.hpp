@@ -1,7 +1,7 @@
 // paged_decode for gfx950: split-K decode attention over a paged KV cache.
 //
 // Semantics follow the reference's paged_decode (src/kernels.metal:35-121): a workgroup owns one
-// partition of part_tokens tokens of one sequence and QG query heads of one KV head, and writes the
+// partition of part_tokens tokens of one sequence and qg query heads of one KV head, and writes the
 // partition's normalised output o / l plus (m, l) to slot (b*H + h)*max_parts + part of the
 // split-K workspace. The mapping onto CDNA4 is this build's own:
 //
@@ -10,9 +10,11 @@
 //    state; the workgroup merges the four wave states at the end, as the reference merges its
 //    simdgroups.
 //  * Both products run on MFMA. Scores come out transposed, S^T = K Q^T, one 16x16 tile per 16
-//    tokens: the tokens are rows, the 16 columns are the QG heads split into a high and a low fp16
+//    tokens: the tokens are rows, the 16 columns are the qg heads split into a high and a low fp16
 //    part (columns 2h, 2h+1), so K is read as stored and q keeps ~22 bits; the MFMA accumulates in
-//    fp32. fp32 caches use v_mfma_f32_16x16x4_f32 on q and K as they are (columns 2h+1 are zero).
+//    fp32. The kernel is built for QG = 1, 2, 4 or 8 heads and serves qg <= QG of them (DecodeParams::qg:
+//    a group of 3 runs the QG = 4 build, of 5, 6 or 7 the QG = 8 build, both as their PART variants,
+//    which read qg at run time); the columns past qg are zero. fp32 caches use v_mfma_f32_16x16x4_f32 on q and K as they are (columns 2h+1 are zero).
 //  * In that layout a lane holds 8 tokens of one column, which is exactly its share of the P^T
 //    operand of O^T = V^T P^T (v_mfma_f32_16x16x32_f16 over 32 tokens): p = exp2(s - m) never
 //    leaves the lane, split into high and low fp16 parts like q. V^T comes from LDS through the
@@ -323,7 +325,7 @@ __device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int bat
 // partitions' tiles in order; each partition's tiles go to the same waves, in the same order, as in
 // a workgroup of its own (part_tokens is a multiple of 32 * waves), and a wave starts its second
 // partition from a fresh state, so every partition gets the same bits either way.
-template <int KIND, int D, int QG, bool FAST, bool LOADS = false, bool PAIR = false>
+template <int KIND, int D, int QG, bool FAST, bool LOADS = false, bool PAIR = false, bool PART = false>
 __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(KIND == KV_I8 && FAST && !LOADS && !PAIR && QG > 1 ? 3 : 2))) void paged_decode_kernel(DecodeParams p) {
     using T = KvT<KIND, D>;
     using R = TileRegs<KIND, D>;
@@ -346,7 +348,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     __shared__ __attribute__((aligned(16))) float s_part[PAIR ? W : 1][PAIR ? QG * D : 4];
     __shared__ float2 s_ml2[PAIR ? W : 1][QG];
 
-    // Grid (H / QG, B, max_parts), head group fastest: workgroups go to the 8 XCDs round robin by
+    // Grid (H / qg, B, max_parts), head group fastest: workgroups go to the 8 XCDs round robin by
     // linear id, so consecutive ids (one partition of consecutive head groups and sequences) spread
     // every partition's work over all XCDs. With the partition fastest, the XCD followed the
     // partition index, and the partitions that short sequences leave empty left XCDs idle (c5
@@ -363,14 +365,17 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         b = it.b;
         part = it.part;
     }
-    const int h0 = blockIdx.x * QG;
+    // Query heads of this workgroup: QG, or with PART the group's p.qg < QG (the MFMA columns past
+    // them idle). A full group keeps the count a constant, so its column masks fold away.
+    const int NQ = PART ? p.qg : QG;
+    const int h0 = blockIdx.x * NQ;
     const int len = live_len(p.seq_lens, b, p.len_cap);  // nparts <= max_parts, t1 <= max_blocks * P
     const int t0 = part * p.part_tokens;
     const int H = p.num_heads, Hkv = p.num_kv_heads, P = p.page_size;
     if (t0 >= len) {  // uniform over the workgroup, before any barrier
         // fused merge: an empty sequence attends to nothing, its output is exactly 0
         if (p.out && len == 0 && part == 0)
-            for (int idx = threadIdx.x; idx < QG * D; idx += 64 * W) p.out[((size_t)b * H + h0) * D + idx] = 0.0f;
+            for (int idx = threadIdx.x; idx < NQ * D; idx += 64 * W) p.out[((size_t)b * H + h0) * D + idx] = 0.0f;
         return;
     }
     const int t1 = min(len, t0 + G * p.part_tokens);
@@ -502,7 +507,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // the tiles' latency. (vmcnt counts loads in the order they were issued: a q load issued
     // after the tiles could only be waited for together with them.)
     const int hh = c >> 1, hl = c & 1;
-    const bool qcol = hh < QG;
+    const bool qcol = hh < NQ;
     const float* qp = p.q + ((size_t)b * H + h0 + (qcol ? hh : 0)) * D;
     float up = 1.0f;  // scores are MFMA results times `up` (a power of two; int8: per head)
     half8_t aq16[KIND == KV_F16 ? NJ : 1];
@@ -876,7 +881,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     static_assert(QG * D / 4 <= 64 * W, "one 16-byte output chunk per thread");
     for (int gp = 0; gp < ng; ++gp) {  // uniform
       const bool lastp = gp == ng - 1;
-      if (threadIdx.x < QG * D / 4) {
+      if (threadIdx.x < NQ * D / 4) {
         const int eh = threadIdx.x / (D / 4), ed = threadIdx.x % (D / 4);
         auto wml = [&](int w) { return lastp ? s_ml[w][eh] : s_ml2[PAIR ? w : 0][eh]; };
         auto wacc = [&](int w) {
@@ -898,7 +903,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         const float4 r = make_float4(o.x / L, o.y / L, o.z / L, o.w / L);
         const size_t slot0 = ((size_t)b * H + h0) * p.max_parts + part + gp;  // head h0's slot
         const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(
-            p.part_out + slot0 * D, (short)0, QG * p.max_parts * D * 4, 0x00020000);
+            p.part_out + slot0 * D, (short)0, NQ * p.max_parts * D * 4, 0x00020000);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, r), rpo,
                                                (eh * p.max_parts * D + 4 * ed) * 4, 0, kScopeAgent);
         if (ed == 0) {
@@ -953,9 +958,9 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     float2* s_pml = reinterpret_cast<float2*>(&s_v[0][0]);  // [QG][nparts]
     const size_t gbase = ((size_t)b * H + h0) * p.max_parts;  // first slot of head h0
     const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(
-        p.part_out + gbase * D, (short)0, QG * p.max_parts * D * 4, 0x00020000);
+        p.part_out + gbase * D, (short)0, NQ * p.max_parts * D * 4, 0x00020000);
     const int e = threadIdx.x, eh = e / (D / 4), ed = e % (D / 4);
-    const bool owner = e < QG * D / 4;
+    const bool owner = e < NQ * D / 4;
     auto row = [&](int i) {  // partition i's chunk of this thread (zeros past the group's slots)
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                               rpo, ((eh * p.max_parts + i) * D + 4 * ed) * 4, 0, kScopeAgent));
@@ -1001,12 +1006,12 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     }
     float4 pre[kPre];
     for (int j = 0; j < kPre; ++j) pre[j] = row(j);
-    for (int x = threadIdx.x; x < QG * nparts; x += 64 * W) {
+    for (int x = threadIdx.x; x < NQ * nparts; x += 64 * W) {
         const size_t slot = gbase + (size_t)(x / nparts) * p.max_parts + x % nparts;
         s_pml[x] = make_float2(load_agent(&p.part_ml[slot].x), load_agent(&p.part_ml[slot].y));
     }
     __syncthreads();
-    for (int x = threadIdx.x; x < QG * nparts; x += 64 * W) {
+    for (int x = threadIdx.x; x < NQ * nparts; x += 64 * W) {
         const float2* mrow = s_pml + (x / nparts) * nparts;
         float M = kNegBig;
         for (int i = 0; i < nparts; ++i) M = fmaxf(M, mrow[i].x);
@@ -1035,16 +1040,16 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
 // whenever the grid has more than one per CU. The largest size at which the occupancy calculator
 // gives the variant the decode's count (at most what one workgroup may allocate); computed once per
 // instantiation.
-template <int KIND, int D, int QG, bool PAIR>
+template <int KIND, int D, int QG, bool PAIR, bool PART>
 hipError_t loads_only_lds(size_t* lds) {
     static size_t cached = SIZE_MAX;
     if (cached == SIZE_MAX) {
-        const auto loads = paged_decode_kernel<KIND, D, QG, true, true, PAIR>;
+        const auto loads = paged_decode_kernel<KIND, D, QG, true, true, PAIR, PART>;
         const int threads = 64 * decode_waves(KIND);
         int occ = 0, dev = 0, lds_cu = 0, lds_wg = 0;
         hipFuncAttributes fa{};
         hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &occ, paged_decode_kernel<KIND, D, QG, true, false, PAIR>, threads, 0);
+            &occ, paged_decode_kernel<KIND, D, QG, true, false, PAIR, PART>, threads, 0);
         if (e == hipSuccess) e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_wg, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
@@ -1069,44 +1074,48 @@ hipError_t loads_only_lds(size_t* lds) {
     return hipSuccess;
 }
 
-template <int KIND, int D, int QG, bool FAST, bool PAIR>
+template <int KIND, int D, int QG, bool FAST, bool PAIR, bool PART>
 hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
     const int gz = PAIR ? (p.max_parts + 1) / 2 : p.max_parts;
-    const dim3 grid(p.num_heads / QG, p.ragged_items ? p.ragged_items : batch, p.ragged_items ? 1 : gz);
+    const dim3 grid(p.num_heads / p.qg, p.ragged_items ? p.ragged_items : batch, p.ragged_items ? 1 : gz);
     if (p.loads_only) {  // tile-aligned pages only
         if constexpr (!FAST) {
             return hipErrorInvalidValue;
         } else {
             size_t lds = 0;
-            if (const hipError_t e = loads_only_lds<KIND, D, QG, PAIR>(&lds); e != hipSuccess) return e;
-            launch_marked_lds(paged_decode_kernel<KIND, D, QG, true, true, PAIR>, grid, dim3(64 * decode_waves(KIND)),
+            if (const hipError_t e = loads_only_lds<KIND, D, QG, PAIR, PART>(&lds); e != hipSuccess) return e;
+            launch_marked_lds(paged_decode_kernel<KIND, D, QG, true, true, PAIR, PART>, grid, dim3(64 * decode_waves(KIND)),
                               lds, s, m, p);
         }
     } else {
-        launch_marked(paged_decode_kernel<KIND, D, QG, FAST, false, PAIR>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
+        launch_marked(paged_decode_kernel<KIND, D, QG, FAST, false, PAIR, PART>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
     }
     return hipGetLastError();
 }
 
 // Two partitions per workgroup (DecodeParams::pair): tile-aligned f16 and i8 caches, plain grid only.
-template <int KIND, int D, int QG>
+template <int KIND, int D, int QG, bool PART>
 hipError_t launch_qg(bool fast, const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
-    if (!fast) return p.pair ? hipErrorInvalidValue : launch_one<KIND, D, QG, false, false>(p, batch, s, m);
+    if (!fast) return p.pair ? hipErrorInvalidValue : launch_one<KIND, D, QG, false, false, PART>(p, batch, s, m);
     if constexpr (KIND != KV_F32) {
-        if (p.pair) return p.ragged_items ? hipErrorInvalidValue : launch_one<KIND, D, QG, true, true>(p, batch, s, m);
+        if (p.pair) return p.ragged_items ? hipErrorInvalidValue : launch_one<KIND, D, QG, true, true, PART>(p, batch, s, m);
     } else {
         if (p.pair) return hipErrorInvalidValue;
     }
-    return launch_one<KIND, D, QG, true, false>(p, batch, s, m);
+    return launch_one<KIND, D, QG, true, false, PART>(p, batch, s, m);
 }
 
 template <int KIND, int D>
 hipError_t launch_for_dim(int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
     switch (qg) {
-        case 1: return launch_qg<KIND, D, 1>(fast, p, batch, s, m);
-        case 2: return launch_qg<KIND, D, 2>(fast, p, batch, s, m);
-        case 4: return launch_qg<KIND, D, 4>(fast, p, batch, s, m);
-        case 8: return launch_qg<KIND, D, 8>(fast, p, batch, s, m);
+        case 1: return launch_qg<KIND, D, 1, false>(fast, p, batch, s, m);
+        case 2: return launch_qg<KIND, D, 2, false>(fast, p, batch, s, m);
+        case 3: return launch_qg<KIND, D, 4, true>(fast, p, batch, s, m);
+        case 4: return launch_qg<KIND, D, 4, false>(fast, p, batch, s, m);
+        case 5:
+        case 6:
+        case 7: return launch_qg<KIND, D, 8, true>(fast, p, batch, s, m);
+        case 8: return launch_qg<KIND, D, 8, false>(fast, p, batch, s, m);
         default: return hipErrorInvalidValue;
     }
 }

@@ -211,9 +211,7 @@ int validate_paged(const kvb_paged_args* a) {
 }
 
 int query_heads_per_group(const kvb_paged_args* a) {
-    const int G = a->num_heads / a->num_kv_heads;
-    if (!a->share_kv) return 1;
-    return G % 8 == 0 ? 8 : G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
+    return kvb_heads_per_workgroup(a->num_heads, a->num_kv_heads, a->share_kv);
 }
 
 // Grows the fused-merge counters to B * H ints, zeroed (the kernel leaves them at 0).
@@ -270,6 +268,7 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     p.num_heads = a->num_heads;
     p.num_kv_heads = a->num_kv_heads;
     p.group = a->num_heads / a->num_kv_heads;
+    p.qg = qg;
     p.page_size = a->page_size;
     p.page_div = kvbk::make_fast_div((uint32_t)a->page_size);
     p.tile_in_page = a->page_size % 32 == 0 && part % 32 == 0;
@@ -430,6 +429,15 @@ int kvb_auto_part_tokens(int batch, int num_kv_heads, int max_len) {
     int part = 512;
     while (part > 64 && (size_t)batch * num_kv_heads * (size_t)((max_len + part - 1) / part) < 512) part /= 2;
     return part;
+}
+
+int kvb_heads_per_workgroup(int num_heads, int num_kv_heads, int share_kv) {
+    if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0) return -1;
+    if (!share_kv) return 1;
+    const int group = num_heads / num_kv_heads;
+    for (int g = 8; g > 1; --g)
+        if (group % g == 0) return g;
+    return 1;
 }
 
 int kvb_paged_max_parts(const kvb_paged_args* a) {

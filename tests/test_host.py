@@ -214,3 +214,33 @@ def test_c_abi_auto_part_tokens_thresholds(kvb, oracle):
         for hkv in (1, 2, 8):
             for L in list(range(0, 5000, 37)) + [32768, 100000]:
                 assert kvb.auto_part_tokens(b, hkv, L) == oracle.auto_part_tokens(b, hkv, L)
+
+
+def test_heads_per_workgroup(kvb):
+    """kvb_heads_per_workgroup: the largest divisor of the group that is at most 8 (one workgroup
+    reads each K/V page for that many query heads), 1 without share_kv, -1 for shapes the decode
+    refuses. Spot values, then every group to 64 against a brute-force search over 8..1."""
+    spot = {1: 1, 2: 2, 3: 3, 4: 4, 5: 5, 6: 6, 7: 7, 8: 8, 9: 3, 10: 5, 11: 1, 12: 6, 13: 1, 14: 7, 15: 5,
+            16: 8, 18: 6, 20: 5, 21: 7, 24: 8, 28: 7, 40: 8, 64: 8}
+    for g, want in spot.items():
+        assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, 1) == want, g
+        assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, 0) == 1
+    for g in range(1, 65):
+        got = kvb.hip.kvb_heads_per_workgroup(g * 2, 2, 1)
+        assert g % got == 0 and got <= 8
+        assert all(g % d != 0 for d in range(got + 1, 9)), g
+    for h, hkv in ((8, 0), (0, 8), (12, 8), (-8, 8), (8, -2)):
+        assert kvb.hip.kvb_heads_per_workgroup(h, hkv, 1) == -1, (h, hkv)
+    assert kvb.heads_per_workgroup(kvb.Shape(2, 56, 8, 128)) == 7
+
+
+def test_partition_policy_counts_live_heads(kvb):
+    """The MI355X partition policy counts workgroups with kvb_heads_per_workgroup. Group 3, batch 1,
+    8 KV heads: one workgroup per KV head, so 8 per partition index, and 256 workgroups need 32
+    partitions of 256 tokens at 8192 tokens (counting a workgroup per query head, 24 per partition
+    index, would stop at 512). Groups 7 and 8 at c4's size both give 4096-token partitions."""
+    s3 = kvb.Shape(1, 24, 8, 128)
+    assert kvb.mi355x_part_tokens(s3, 8192) == 256
+    s7 = kvb.Shape(4, 56, 8, 128)
+    s8 = kvb.Shape(4, 64, 8, 128)
+    assert kvb.mi355x_part_tokens(s7, 32768) == kvb.mi355x_part_tokens(s8, 32768) == 4096
