@@ -325,7 +325,8 @@ __device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int bat
 // partitions' tiles in order; each partition's tiles go to the same waves, in the same order, as in
 // a workgroup of its own (part_tokens is a multiple of 32 * waves), and a wave starts its second
 // partition from a fresh state, so every partition gets the same bits either way.
-template <int KIND, int D, int QG, bool FAST, bool LOADS = false, bool PAIR = false, bool PART = false>
+template <int KIND, int D, int QG, bool FAST, bool LOADS = false, bool PAIR = false, bool PART = false,
+          bool SHARE = false>
 __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(KIND == KV_I8 && FAST && !LOADS && !PAIR && QG > 1 ? 3 : 2))) void paged_decode_kernel(DecodeParams p) {
     using T = KvT<KIND, D>;
     using R = TileRegs<KIND, D>;
@@ -337,6 +338,11 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // fp32 tiles are too large for more than one. (Three for int8, whose tiles are half an fp16
     // tile, spill at head_dim 128 and measured slower.)
     constexpr int NBUF = F32 ? 1 : 2;
+    // Cache policy of the K/V tile loads: non-temporal when one workgroup reads each page; ordinary
+    // with SHARE, whose sibling workgroups read each page again from L2 (MI355X, c4's size with
+    // groups of 16: 163.5 -> 106.9 us fp16, 88.2 -> 68.0 int8, against 133.7 / 80.9 with the sibling
+    // order alone; non-temporal stays for one workgroup per KV head: 84.5 us there, 93.9 without).
+    constexpr int kKvPolicy = SHARE ? 0 : kNonTemporal;
 
     // Per wave: the V tile (32 rows of D elements, swizzled); after the loop it holds the wave's
     // final accumulators [QG][D] fp32 for the merge (QG * D * 4 <= 32 * D * LDS_ESZ bytes).
@@ -358,9 +364,28 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     const unsigned lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
 #endif
     constexpr int G = PAIR ? 2 : 1;  // partitions per workgroup
-    int part = blockIdx.z * G, b = blockIdx.y;  // part: the workgroup's first partition
+    // SHARE: a KV head has S = group / qg > 1 workgroups (its query heads in S blocks), which read the
+    // same pages. Their ids are remapped to lie 8 apart, so that they run on one XCD (workgroups go
+    // to the XCDs round robin by linear id) at about the same time, and the later reads of a page
+    // hit that XCD's L2; the loads are then ordinary (temporal) loads. In blocks of 8 * S ids: id
+    // i of a block is sibling i / 8 of unit 8 * block + i % 8, units being (KV head, y, z) in the
+    // plain order (KV head fastest). Only when the units fill whole blocks; otherwise the plain order.
+    int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+    if constexpr (SHARE) {
+        const unsigned S = p.group / (PART ? p.qg : QG), X = gridDim.x, Y = gridDim.y, Z = gridDim.z;
+        const unsigned XK = X / S;  // KV heads
+        if (S > 1 && (XK * Y * Z) % 8 == 0) {
+            const unsigned id = blockIdx.x + X * (blockIdx.y + Y * blockIdx.z);
+            const unsigned blk = id / (8 * S), within = id % (8 * S);
+            const unsigned unit = 8 * blk + within % 8, yz = unit / XK;
+            bx = (int)((unit % XK) * S + within / 8);
+            by = (int)(yz % Y);
+            bz = (int)(yz / Y);
+        }
+    }
+    int part = bz * G, b = by;  // part: the workgroup's first partition
     if (p.ragged_items) {
-        const WorkItem it = ragged_item(p.seq_lens, p.batch, p.part_tokens, p.len_cap, blockIdx.y, gridDim.y);
+        const WorkItem it = ragged_item(p.seq_lens, p.batch, p.part_tokens, p.len_cap, by, gridDim.y);
         if (it.b < 0 || it.b >= p.batch || it.part >= p.max_parts) return;  // uniform, before any barrier
         b = it.b;
         part = it.part;
@@ -368,7 +393,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // Query heads of this workgroup: QG, or with PART the group's p.qg < QG (the MFMA columns past
     // them idle). A full group keeps the count a constant, so its column masks fold away.
     const int NQ = PART ? p.qg : QG;
-    const int h0 = blockIdx.x * NQ;
+    const int h0 = bx * NQ;
     const int len = live_len(p.seq_lens, b, p.len_cap);  // nparts <= max_parts, t1 <= max_blocks * P
     const int t0 = part * p.part_tokens;
     const int H = p.num_heads, Hkv = p.num_kv_heads, P = p.page_size;
@@ -450,10 +475,10 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                     const_cast<char*>(vbase + row0 * D * T::ESZ), (short)0, nbytes, 0x00020000);
                 for (int m = 0; m < T::KLOADS; ++m)
                     r.k[h][m] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                              rk, (c * D + T::kdoff(m, q4)) * T::ESZ, 0, kNonTemporal));
+                                                              rk, (c * D + T::kdoff(m, q4)) * T::ESZ, 0, kKvPolicy));
                 for (int i = 0; i < NV; ++i)
                     r.v[h][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                              rv, (i * (64 / VL) + lane / VL) * D * T::ESZ + (lane % VL) * 16, 0, kNonTemporal));
+                                                              rv, (i * (64 / VL) + lane / VL) * D * T::ESZ + (lane % VL) * 16, 0, kKvPolicy));
                 if constexpr (KIND == KV_I8) {
                     // (with tile_in_page the second half's scales are the first half's: the arithmetic
                     // selects them; copying the register here would wait for its load, and so for
@@ -939,7 +964,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // the whole L2 of the XCD in every workgroup (buffer_wbl2 / buffer_inv): 140 us per c4 step.
     __shared__ int s_last;
     const int nparts = (len + p.part_tokens - 1) / p.part_tokens;
-    int* counter = p.counters + (size_t)b * gridDim.x + blockIdx.x;
+    int* counter = p.counters + (size_t)b * gridDim.x + bx;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0)
@@ -1040,16 +1065,16 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
 // whenever the grid has more than one per CU. The largest size at which the occupancy calculator
 // gives the variant the decode's count (at most what one workgroup may allocate); computed once per
 // instantiation.
-template <int KIND, int D, int QG, bool PAIR, bool PART>
+template <int KIND, int D, int QG, bool PAIR, bool PART, bool SHARE>
 hipError_t loads_only_lds(size_t* lds) {
     static size_t cached = SIZE_MAX;
     if (cached == SIZE_MAX) {
-        const auto loads = paged_decode_kernel<KIND, D, QG, true, true, PAIR, PART>;
+        const auto loads = paged_decode_kernel<KIND, D, QG, true, true, PAIR, PART, SHARE>;
         const int threads = 64 * decode_waves(KIND);
         int occ = 0, dev = 0, lds_cu = 0, lds_wg = 0;
         hipFuncAttributes fa{};
         hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &occ, paged_decode_kernel<KIND, D, QG, true, false, PAIR, PART>, threads, 0);
+            &occ, paged_decode_kernel<KIND, D, QG, true, false, PAIR, PART, SHARE>, threads, 0);
         if (e == hipSuccess) e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_wg, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
@@ -1074,7 +1099,7 @@ hipError_t loads_only_lds(size_t* lds) {
     return hipSuccess;
 }
 
-template <int KIND, int D, int QG, bool FAST, bool PAIR, bool PART>
+template <int KIND, int D, int QG, bool FAST, bool PAIR, bool PART, bool SHARE>
 hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
     const int gz = PAIR ? (p.max_parts + 1) / 2 : p.max_parts;
     const dim3 grid(p.num_heads / p.qg, p.ragged_items ? p.ragged_items : batch, p.ragged_items ? 1 : gz);
@@ -1083,39 +1108,46 @@ hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Mar
             return hipErrorInvalidValue;
         } else {
             size_t lds = 0;
-            if (const hipError_t e = loads_only_lds<KIND, D, QG, PAIR, PART>(&lds); e != hipSuccess) return e;
-            launch_marked_lds(paged_decode_kernel<KIND, D, QG, true, true, PAIR, PART>, grid, dim3(64 * decode_waves(KIND)),
+            if (const hipError_t e = loads_only_lds<KIND, D, QG, PAIR, PART, SHARE>(&lds); e != hipSuccess) return e;
+            launch_marked_lds(paged_decode_kernel<KIND, D, QG, true, true, PAIR, PART, SHARE>, grid, dim3(64 * decode_waves(KIND)),
                               lds, s, m, p);
         }
     } else {
-        launch_marked(paged_decode_kernel<KIND, D, QG, FAST, false, PAIR, PART>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
+        launch_marked(paged_decode_kernel<KIND, D, QG, FAST, false, PAIR, PART, SHARE>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
     }
     return hipGetLastError();
 }
 
 // Two partitions per workgroup (DecodeParams::pair): tile-aligned f16 and i8 caches, plain grid only.
-template <int KIND, int D, int QG, bool PART>
+template <int KIND, int D, int QG, bool PART, bool SHARE = false>
 hipError_t launch_qg(bool fast, const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
-    if (!fast) return p.pair ? hipErrorInvalidValue : launch_one<KIND, D, QG, false, false, PART>(p, batch, s, m);
+    if (!fast) return p.pair ? hipErrorInvalidValue : launch_one<KIND, D, QG, false, false, PART, SHARE>(p, batch, s, m);
     if constexpr (KIND != KV_F32) {
-        if (p.pair) return p.ragged_items ? hipErrorInvalidValue : launch_one<KIND, D, QG, true, true, PART>(p, batch, s, m);
+        if (p.pair) return p.ragged_items ? hipErrorInvalidValue : launch_one<KIND, D, QG, true, true, PART, SHARE>(p, batch, s, m);
     } else {
         if (p.pair) return hipErrorInvalidValue;
     }
-    return launch_one<KIND, D, QG, true, false, PART>(p, batch, s, m);
+    return launch_one<KIND, D, QG, true, false, PART, SHARE>(p, batch, s, m);
 }
 
 template <int KIND, int D>
 hipError_t launch_for_dim(int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
+    const bool sib = p.group > qg;  // more than one workgroup per KV head
     switch (qg) {
+        // SHARE builds where a KV head has more than one workgroup and one workgroup serves 3 or 5-8
+        // heads (groups 9, 10, 12, 14, 16, 24, 32, ...); groups whose workgroups serve 1, 2 or 4
+        // heads each (11, 13, 22, 44, ...) keep the plain order and non-temporal loads.
         case 1: return launch_qg<KIND, D, 1, false>(fast, p, batch, s, m);
         case 2: return launch_qg<KIND, D, 2, false>(fast, p, batch, s, m);
-        case 3: return launch_qg<KIND, D, 4, true>(fast, p, batch, s, m);
+        case 3: return sib ? launch_qg<KIND, D, 4, true, true>(fast, p, batch, s, m)
+                           : launch_qg<KIND, D, 4, true>(fast, p, batch, s, m);
         case 4: return launch_qg<KIND, D, 4, false>(fast, p, batch, s, m);
         case 5:
         case 6:
-        case 7: return launch_qg<KIND, D, 8, true>(fast, p, batch, s, m);
-        case 8: return launch_qg<KIND, D, 8, false>(fast, p, batch, s, m);
+        case 7: return sib ? launch_qg<KIND, D, 8, true, true>(fast, p, batch, s, m)
+                           : launch_qg<KIND, D, 8, true>(fast, p, batch, s, m);
+        case 8: return sib ? launch_qg<KIND, D, 8, false, true>(fast, p, batch, s, m)
+                           : launch_qg<KIND, D, 8, false>(fast, p, batch, s, m);
         default: return hipErrorInvalidValue;
     }
 }

@@ -1,4 +1,4 @@
-"""GQA groups that are not powers of two (3, 5, 6, 7, 12, 14). One paged_decode workgroup serves
+"""GQA groups other than 1, 2, 4 and 8 (3, 5, 6, 7, 9, 12, 14, 16, 32). One paged_decode workgroup serves
 kvb_heads_per_workgroup query heads of a KV head, the largest divisor of the group that is at most
 8, so it reads each K/V page once for all of them (src/metal_attn.mm:64-80 builds its kernel with
 QG = GROUP for any group). It runs the kernel built for the next of 1, 2, 4 and 8 heads, whose
@@ -6,7 +6,9 @@ MFMA columns past those heads stay idle. Checked for every storage type:
 - the output against the oracle, on the plain grid (fused merge, one and two partitions per
   workgroup), the ragged grid, and a layout whose page is not a tile multiple;
 - the fused step against the two-kernel form, bit for bit;
-- every workspace slot against the oracle's partition state."""
+- every workspace slot against the oracle's partition state;
+- groups past 8, whose KV heads have several workgroups (placed on one XCD and reading with ordinary
+  loads): each workgroup's heads bit for bit against a group-8 run of the same heads."""
 import numpy as np
 import pytest
 
@@ -23,6 +25,9 @@ SHAPES = [
     ((2, 56, 8, 128), 7),
     ((1, 24, 2, 128), 6),   # group 12: two workgroups per KV head
     ((1, 28, 2, 64), 7),    # group 14: two workgroups per KV head
+    ((1, 18, 2, 64), 3),    # group 9: three workgroups of 3 per KV head
+    ((1, 32, 2, 128), 8),   # group 16: two workgroups of 8
+    ((1, 64, 2, 128), 8),   # group 32: four workgroups of 8
 ]
 IDS = [f"H{s[1]}-Hkv{s[2]}-D{s[3]}" for s, _ in SHAPES]
 
@@ -114,3 +119,38 @@ def test_groups_workspace_slots(gpu, oracle, shape, qg, kv):
                 assert abs(part_ml[b, h, p, 1] - l) <= 1e-5 * l, (b, h, p)
                 assert np.abs(part_out[b, h, p] - o).max() <= 2e-5 * max(1.0, vmax), (b, h, p)
     progress(f"[groups] workspace {shape} {kv}: qg {qg}, {B * H * max_parts} slots")
+
+
+@pytest.mark.parametrize("kv", ["f16", "i8", "f32"])
+# (KV head, sequence or work item, partition) units: 16, 32, 24 and 64 fill blocks of 8 (the
+# sibling order); the ragged [500, 300, 120] at 160 has 2 x 7 = 14 (the plain order)
+@pytest.mark.parametrize("lens,part", [([1000, 1000], 256), ([1000, 1000], 128), ([777, 65, 300, 1], 128),
+                                       ([4096, 4096, 4096, 4096], 512), ([500, 300, 120], 160)])
+def test_sibling_workgroups_give_group8_bits(gpu, kv, lens, part):
+    """Group 16 runs two workgroups of 8 heads per KV head. Each gives the same bits as a group-8
+    run over the same K/V with its 8 heads as the group, with the sibling order (when the
+    (KV head, sequence, partition) units fill blocks of 8) and without it."""
+    kvb = gpu
+    B = len(lens)
+    w16 = kvb.Workload(kvb.Shape(B, 32, 2, 128), kv, lens, seed=len(lens) * 31 + part)
+    k, v = w16.k, w16.v  # as stored (fp16) or before quantisation (int8, fp32)
+    c16 = kvb.PagedCache(w16, 16, 3, pool_factor=1.5, poison=True)
+    dev = kvb.DeviceCase(w16, c16)
+    dev.out.fill(0xFF)
+    dev.run(part)
+    out16 = dev.output().copy()
+    units = 2 * B * dev.max_parts(part)
+    dev.free()
+    for half in (0, 1):
+        heads = [16 * g + 8 * half + j for g in range(2) for j in range(8)]
+        w8 = kvb.Workload.from_arrays(kv, lens, w16.q[:, heads], k, v)
+        c8 = kvb.PagedCache(w8, 16, 5, pool_factor=1.5, poison=True)
+        if kv == "i8":  # the same pages give the same bytes and scales
+            assert np.array_equal(c8.dequantized(w8)[0], c16.dequantized(w16)[0])
+        d8 = kvb.DeviceCase(w8, c8)
+        d8.out.fill(0xFF)
+        d8.run(part)
+        out8 = d8.output()
+        d8.free()
+        assert np.array_equal(out16[:, heads].view(np.uint32), out8.view(np.uint32)), half
+    progress(f"[groups] group 16 = 2 x group 8 bits, {kv} lens {lens} part {part} ({units} units)")
