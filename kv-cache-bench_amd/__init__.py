@@ -83,7 +83,7 @@ _SIGS = {
     "kvb_copy_d2h": ([_p, _p, _sz], _i),
     "kvb_fill_bytes": ([_p, _i, _sz], _i),
     "kvb_auto_part_tokens": ([_i, _i, _i], _i),
-    "kvb_heads_per_workgroup": ([_i, _i, _i], _i),
+    "kvb_heads_per_workgroup": ([_i, _i, _i, _i], _i),
     "kvb_paged_max_parts": ([_PA], _i),
     "kvb_paged_workspace_bytes": ([_PA], _sz),
     "kvb_check_paged": ([_PA], _i),
@@ -169,10 +169,12 @@ def auto_part_tokens(batch, num_kv_heads, max_len) -> int:
     return hip.kvb_auto_part_tokens(batch, num_kv_heads, max_len)
 
 
-def heads_per_workgroup(shape, share_kv=True) -> int:
-    """Query heads one paged_decode workgroup serves (kvb_heads_per_workgroup): the largest divisor
-    of the group that is at most 8, or 1 without share_kv."""
-    return hip.kvb_heads_per_workgroup(shape.num_heads, shape.num_kv_heads, int(share_kv))
+def heads_per_workgroup(shape, kv_type=KV_F16, share_kv=True) -> int:
+    """Query heads one paged_decode workgroup serves (kvb_heads_per_workgroup): 16 for a multiple of
+    16 with an f16 cache, else the largest divisor of the group that is at most 8; 1 without
+    share_kv."""
+    return hip.kvb_heads_per_workgroup(shape.num_heads, shape.num_kv_heads, KV_BY_NAME.get(kv_type, kv_type),
+                                       int(share_kv))
 
 
 def mi355x_part_tokens(shape, max_len, min_groups=256, min_part=256, max_part=4096) -> int:

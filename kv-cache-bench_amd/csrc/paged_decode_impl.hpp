@@ -327,13 +327,20 @@ __device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int bat
 // partition from a fresh state, so every partition gets the same bits either way.
 template <int KIND, int D, int QG, bool FAST, bool LOADS = false, bool PAIR = false, bool PART = false,
           bool SHARE = false>
-__global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(KIND == KV_I8 && FAST && !LOADS && !PAIR && QG > 1 ? 3 : 2))) void paged_decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(QG > 8 ? 1 : KIND == KV_I8 && FAST && !LOADS && !PAIR && QG > 1 ? 3 : 2))) void paged_decode_kernel(DecodeParams p) {
     using T = KvT<KIND, D>;
     using R = TileRegs<KIND, D>;
     constexpr int W = decode_waves(KIND);
     constexpr int NJ = T::NJ, VL = T::VL, NV = T::NV, NMB = D / 16;
     constexpr bool F32 = KIND == KV_F32;
-    static_assert(QG == 1 || QG == 2 || QG == 4 || QG == 8, "QG must be 1, 2, 4 or 8");
+    static_assert(QG == 1 || QG == 2 || QG == 4 || QG == 8 || (QG == 16 && KIND == KV_F16),
+                  "QG must be 1, 2, 4, 8 or (fp16) 16");
+    // Blocks of 8 query heads: the score MFMA's 16 columns hold 8 heads (a high and a low column
+    // each), so QG 16 runs two blocks over each tile: both read the tile's K registers and V reads.
+    // fp16 only: at c4's size with 16 query heads per KV head, fp16 ran 88.4 us this way against
+    // 106.3 us as two workgroups of 8 (SHARE); int8 ran 149.3 us against 71.4 (its arithmetic per
+    // tile, doubled, no longer hides under the loads, and its accumulators spill to AGPRs).
+    constexpr int HB = QG > 8 ? QG / 8 : 1;
     // Tile register buffers per wave: one computed while the next is loaded (see the tile walk).
     // fp32 tiles are too large for more than one. (Three for int8, whose tiles are half an fp16
     // tile, spill at head_dim 128 and measured slower.)
@@ -345,9 +352,10 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     constexpr int kKvPolicy = SHARE ? 0 : kNonTemporal;
 
     // Per wave: the V tile (32 rows of D elements, swizzled); after the loop it holds the wave's
-    // final accumulators [QG][D] fp32 for the merge (QG * D * 4 <= 32 * D * LDS_ESZ bytes).
-    static_assert(QG * 4 <= kTok * T::LDS_ESZ, "merge buffer must fit in the V tile");
-    __shared__ __attribute__((aligned(16))) unsigned char s_v[W][kTok * D * T::LDS_ESZ];
+    // final accumulators [QG][D] fp32 for the merge: the larger of the two (QG 16 int8: the
+    // accumulators).
+    constexpr int SVB = kTok * T::LDS_ESZ >= QG * 4 ? kTok * D * T::LDS_ESZ : QG * D * 4;
+    __shared__ __attribute__((aligned(16))) unsigned char s_v[W][SVB];
     __shared__ float2 s_ml[W][QG];
     // PAIR: each wave's state for the first partition, [QG][D] fp32 and (m, l), as the V tile holds
     // the last partition's after the walk
@@ -531,17 +539,21 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // Its loads go out first, then the wave's first NBUF - 1 tiles; the q split then runs under
     // the tiles' latency. (vmcnt counts loads in the order they were issued: a q load issued
     // after the tiles could only be waited for together with them.)
+    // Head block hb's column c holds head 8 hb + c / 2.
     const int hh = c >> 1, hl = c & 1;
-    const bool qcol = hh < NQ;
-    const float* qp = p.q + ((size_t)b * H + h0 + (qcol ? hh : 0)) * D;
-    float up = 1.0f;  // scores are MFMA results times `up` (a power of two; int8: per head)
-    half8_t aq16[KIND == KV_F16 ? NJ : 1];
+    bool qcol[HB];
+    for (int hb = 0; hb < HB; ++hb) qcol[hb] = 8 * hb + hh < NQ;
+    float up[HB];  // scores are MFMA results times `up` (a power of two; int8: per head)
+    half8_t aq16[HB][KIND == KV_F16 ? NJ : 1];
     float aq32[F32 ? NJ : 1];
-    i32x4_t aq8[KIND == KV_I8 ? 2 * T::KLOADS : 1];  // int8: q digits, first and second score MFMA
+    i32x4_t aq8[HB][KIND == KV_I8 ? 2 * T::KLOADS : 1];  // int8: q digits, first and second score MFMA
     constexpr int QS = F32 ? 1 : 8;  // q elements per MFMA slot
-    float qv[NJ][QS];                // raw loads only: any use before the barrier below would wait for them
-    for (int j = 0; j < NJ; ++j)
-        for (int s = 0; s < QS; ++s) qv[j][s] = qp[T::dslot(j, q4, s)];
+    float qv[HB][NJ][QS];            // raw loads only: any use before the barrier below would wait for them
+    for (int hb = 0; hb < HB; ++hb) {
+        const float* qp = p.q + ((size_t)b * H + h0 + (qcol[hb] ? 8 * hb + hh : 0)) * D;
+        for (int j = 0; j < NJ; ++j)
+            for (int s = 0; s < QS; ++s) qv[hb][j][s] = qp[T::dslot(j, q4, s)];
+    }
     // the partition's blocks (and int8 scales) into lanes: their round trip overlaps q's
     if (lanes) {
         const int nb = fast_div(t1 - 1, p.page_div) - bi0 + 1;  // <= kLaneBlocks (host-checked)
@@ -567,69 +579,72 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // their first use, and the q loads past the tiles')
     asm volatile("" ::: "memory");
 
-    for (int j = 0; j < NJ; ++j)
-        for (int s = 0; s < QS; ++s) qv[j][s] = (qcol && (!F32 || hl == 0)) ? qv[j][s] * p.qscale : 0.0f;
-    if constexpr (F32) {
-        for (int j = 0; j < NJ; ++j) aq32[j] = qv[j][0];
-    } else {
-        float amax = 0.0f;
-        bool finite = true;
+    for (int hb = 0; hb < HB; ++hb) {
+        up[hb] = 1.0f;
         for (int j = 0; j < NJ; ++j)
-            for (int s = 0; s < 8; ++s) {
-                const float a = fabsf(qv[j][s]);
-                amax = fmaxf(amax, a);
-                finite = finite && a <= 3.402823466e38f;
-            }
-        // fp16: one scale for the wave (floating point keeps each element's relative precision).
-        // int8: one per head, over the 8 lanes holding it (columns 2h, 2h + 1, all q4): the digits
-        // are fixed point, so a head with a small q next to a large one keeps its own precision.
-        if constexpr (KIND == KV_I8) {
-            if (!finite) amax = __builtin_inff();  // (the max carries it to the head's other lanes)
-            amax = max_x16_x32(amax);
-            amax = fmaxf(amax, dpp<kQuadSwap1>(amax));
+            for (int s = 0; s < QS; ++s) qv[hb][j][s] = (qcol[hb] && (!F32 || hl == 0)) ? qv[hb][j][s] * p.qscale : 0.0f;
+        if constexpr (F32) {
+            for (int j = 0; j < NJ; ++j) aq32[j] = qv[hb][j][0];
         } else {
-            amax = wave_max(amax);
-        }
-        int e = 0;
-        if (amax > 0.0f && amax <= 3.402823466e38f) {
-            frexpf(amax, &e);  // amax < 2^e
-            // fp16: the scaled q stays below 2^14, far from overflow; int8: below 2^7, a digit's range
-            e -= KIND == KV_I8 ? 7 : 14;
-        }
-        float down = ldexpf(1.0f, -e);
-        up = ldexpf(1.0f, e);
-        if (KIND == KV_I8 && !(amax <= 3.402823466e38f)) {
-            // a NaN or infinite q element: the head's scores are NaN, as in floating point (the
-            // digits alone would clamp it to a finite value)
-            down = 0.0f;
-            up = __builtin_nanf("");
-        }
-        if constexpr (KIND == KV_F16) {
+            float amax = 0.0f;
+            bool finite = true;
             for (int j = 0; j < NJ; ++j)
                 for (int s = 0; s < 8; ++s) {
-                    const float x = qv[j][s] * down;
-                    const _Float16 hi = (_Float16)x;
-                    const _Float16 lo = (_Float16)(x - (float)hi);
-                    aq16[j][s] = hl ? lo : hi;
+                    const float a = fabsf(qv[hb][j][s]);
+                    amax = fmaxf(amax, a);
+                    finite = finite && a <= 3.402823466e38f;
                 }
-        } else {
-            // int8 scores run on the integer MFMA, K as stored: x = q * down = d0 + d1 / 2^7 +
-            // d2 / 2^14 + err, |err| <= 2^-15, each digit a signed byte (every step is exact in
-            // fp32). Column 2h (hl == 0) carries d0 into the first MFMA and d2 into the second;
-            // column 2h + 1 carries d1 and zeros. Slot t of load m is d = 64 m + 16 q4 + t, as K's.
-            for (int m = 0; m < T::KLOADS; ++m) {
-                uint32_t wa[4] = {0u, 0u, 0u, 0u}, wb[4] = {0u, 0u, 0u, 0u};
-                for (int t = 0; t < 16; ++t) {
-                    const float x = qv[2 * m + (t >> 3)][t & 7] * down;
-                    const float d0 = fminf(fmaxf(__builtin_rintf(x), -127.0f), 127.0f);
-                    const float r1 = (x - d0) * 128.0f;
-                    const float d1 = fminf(fmaxf(__builtin_rintf(r1), -127.0f), 127.0f);
-                    const float d2 = fminf(fmaxf(__builtin_rintf((r1 - d1) * 128.0f), -127.0f), 127.0f);
-                    wa[t >> 2] |= (uint32_t)(uint8_t)(int8_t)(int)(hl ? d1 : d0) << (8 * (t & 3));
-                    wb[t >> 2] |= (hl ? 0u : (uint32_t)(uint8_t)(int8_t)(int)d2) << (8 * (t & 3));
+            // fp16: one scale for the wave (floating point keeps each element's relative precision).
+            // int8: one per head, over the 8 lanes holding it (columns 2h, 2h + 1, all q4): the digits
+            // are fixed point, so a head with a small q next to a large one keeps its own precision.
+            if constexpr (KIND == KV_I8) {
+                if (!finite) amax = __builtin_inff();  // (the max carries it to the head's other lanes)
+                amax = max_x16_x32(amax);
+                amax = fmaxf(amax, dpp<kQuadSwap1>(amax));
+            } else {
+                amax = wave_max(amax);
+            }
+            int e = 0;
+            if (amax > 0.0f && amax <= 3.402823466e38f) {
+                frexpf(amax, &e);  // amax < 2^e
+                // fp16: the scaled q stays below 2^14, far from overflow; int8: below 2^7, a digit's range
+                e -= KIND == KV_I8 ? 7 : 14;
+            }
+            float down = ldexpf(1.0f, -e);
+            up[hb] = ldexpf(1.0f, e);
+            if (KIND == KV_I8 && !(amax <= 3.402823466e38f)) {
+                // a NaN or infinite q element: the head's scores are NaN, as in floating point (the
+                // digits alone would clamp it to a finite value)
+                down = 0.0f;
+                up[hb] = __builtin_nanf("");
+            }
+            if constexpr (KIND == KV_F16) {
+                for (int j = 0; j < NJ; ++j)
+                    for (int s = 0; s < 8; ++s) {
+                        const float x = qv[hb][j][s] * down;
+                        const _Float16 hi = (_Float16)x;
+                        const _Float16 lo = (_Float16)(x - (float)hi);
+                        aq16[hb][j][s] = hl ? lo : hi;
+                    }
+            } else {
+                // int8 scores run on the integer MFMA, K as stored: x = q * down = d0 + d1 / 2^7 +
+                // d2 / 2^14 + err, |err| <= 2^-15, each digit a signed byte (every step is exact in
+                // fp32). Column 2h (hl == 0) carries d0 into the first MFMA and d2 into the second;
+                // column 2h + 1 carries d1 and zeros. Slot t of load m is d = 64 m + 16 q4 + t, as K's.
+                for (int m = 0; m < T::KLOADS; ++m) {
+                    uint32_t wa[4] = {0u, 0u, 0u, 0u}, wb[4] = {0u, 0u, 0u, 0u};
+                    for (int t = 0; t < 16; ++t) {
+                        const float x = qv[hb][2 * m + (t >> 3)][t & 7] * down;
+                        const float d0 = fminf(fmaxf(__builtin_rintf(x), -127.0f), 127.0f);
+                        const float r1 = (x - d0) * 128.0f;
+                        const float d1 = fminf(fmaxf(__builtin_rintf(r1), -127.0f), 127.0f);
+                        const float d2 = fminf(fmaxf(__builtin_rintf((r1 - d1) * 128.0f), -127.0f), 127.0f);
+                        wa[t >> 2] |= (uint32_t)(uint8_t)(int8_t)(int)(hl ? d1 : d0) << (8 * (t & 3));
+                        wb[t >> 2] |= (hl ? 0u : (uint32_t)(uint8_t)(int8_t)(int)d2) << (8 * (t & 3));
+                    }
+                    aq8[hb][m] = i32x4_t{(int)wa[0], (int)wa[1], (int)wa[2], (int)wa[3]};
+                    aq8[hb][T::KLOADS + m] = i32x4_t{(int)wb[0], (int)wb[1], (int)wb[2], (int)wb[3]};
                 }
-                aq8[m] = i32x4_t{(int)wa[0], (int)wa[1], (int)wa[2], (int)wa[3]};
-                aq8[T::KLOADS + m] = i32x4_t{(int)wb[0], (int)wb[1], (int)wb[2], (int)wb[3]};
             }
         }
     }
@@ -659,9 +674,13 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // ---- per-wave online-softmax state. Lane (c, q4) holds column c (head c/2) for the tokens
     // 16h + 4*q4 + i of each tile (slot j = 4h + i of the P^T operand): m is uniform over the 8
     // lanes of a head, l is the lane's partial sum over its tokens.
-    float m = kNegBig, l = 0.0f;
-    floatx4_t acc[NMB];
-    for (int mb = 0; mb < NMB; ++mb) acc[mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m[HB], l[HB];
+    floatx4_t acc[HB][NMB];
+    for (int hb = 0; hb < HB; ++hb) {
+        m[hb] = kNegBig;
+        l[hb] = 0.0f;
+        for (int mb = 0; mb < NMB; ++mb) acc[hb][mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
 
     uint32_t lsink = 0;  // LOADS: what the tiles' registers XOR to
     auto compute_tile = [&](const R& r, int tt) {
@@ -678,30 +697,31 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         }
         store_v(r);
         // S^T = K Q^T for both halves
-        floatx4_t S[2];
-        for (int h = 0; h < 2; ++h) {
-            S[h] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-            if constexpr (F32) {
-                for (int j = 0; j < NJ; ++j) {
-                    const uint4 w4 = r.k[h][j >> 2];
-                    const uint32_t w = (j & 3) == 0 ? w4.x : (j & 3) == 1 ? w4.y : (j & 3) == 2 ? w4.z : w4.w;
-                    S[h] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, w), aq32[j], S[h], 0, 0, 0);
+        floatx4_t S[HB][2];
+        for (int h = 0; h < 2; ++h)
+            for (int hb = 0; hb < HB; ++hb) {
+                S[hb][h] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (F32) {
+                    for (int j = 0; j < NJ; ++j) {
+                        const uint4 w4 = r.k[h][j >> 2];
+                        const uint32_t w = (j & 3) == 0 ? w4.x : (j & 3) == 1 ? w4.y : (j & 3) == 2 ? w4.z : w4.w;
+                        S[hb][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, w), aq32[j], S[hb][h], 0, 0, 0);
+                    }
+                } else if constexpr (KIND == KV_F16) {
+                    for (int j = 0; j < NJ; ++j)
+                        S[hb][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, r.k[h][j]), aq16[hb][j], S[hb][h], 0, 0, 0);
+                } else {
+                    // exact integer dot products per digit; the two scaled sums are the column's part
+                    i32x4_t SA = {0, 0, 0, 0}, SB = {0, 0, 0, 0};
+                    for (int m = 0; m < T::KLOADS; ++m) {
+                        const i32x4_t kk = __builtin_bit_cast(i32x4_t, r.k[h][m]);
+                        SA = __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, aq8[hb][m], SA, 0, 0, 0);
+                        SB = __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, aq8[hb][T::KLOADS + m], SB, 0, 0, 0);
+                    }
+                    const float wa = hl ? 1.0f / 128.0f : 1.0f, wb = hl ? 0.0f : 1.0f / 16384.0f;
+                    for (int i = 0; i < 4; ++i) S[hb][h][i] = __builtin_fmaf((float)SB[i], wb, (float)SA[i] * wa);
                 }
-            } else if constexpr (KIND == KV_F16) {
-                for (int j = 0; j < NJ; ++j)
-                    S[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, r.k[h][j]), aq16[j], S[h], 0, 0, 0);
-            } else {
-                // exact integer dot products per digit; the two scaled sums are the column's part
-                i32x4_t SA = {0, 0, 0, 0}, SB = {0, 0, 0, 0};
-                for (int m = 0; m < T::KLOADS; ++m) {
-                    const i32x4_t kk = __builtin_bit_cast(i32x4_t, r.k[h][m]);
-                    SA = __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, aq8[m], SA, 0, 0, 0);
-                    SB = __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, aq8[T::KLOADS + m], SB, 0, 0, 0);
-                }
-                const float wa = hl ? 1.0f / 128.0f : 1.0f, wb = hl ? 0.0f : 1.0f / 16384.0f;
-                for (int i = 0; i < 4; ++i) S[h][i] = __builtin_fmaf((float)SB[i], wb, (float)SA[i] * wa);
             }
-        }
         // int8, FAST: the scales of the two halves (the first's for both with tile_in_page), from the
         // lanes that hold them when the partition's scales are in lanes
         float ksh[2], vsh[2];
@@ -726,52 +746,55 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
             if (vmx > 0.0f) frexpf(vmx, &e);  // vmx < 2^e
             if (e > ve) {  // wave-uniform
                 const float down = ldexpf(1.0f, ve - e);
-                for (int mb = 0; mb < NMB; ++mb) acc[mb] *= down;
+                for (int hb = 0; hb < HB; ++hb)
+                    for (int mb = 0; mb < NMB; ++mb) acc[hb][mb] *= down;
                 ve = e;
                 vdown = ldexpf(1.0f, -e);
             }
         }
         // scores of this lane's 8 tokens for head c/2: high + low columns, scaled, masked
-        float s[8];
-        for (int h = 0; h < 2; ++h)
-            for (int i = 0; i < 4; ++i) {
-                const int j = 4 * h + i;
-                float f = up;
-                if constexpr (KIND == KV_I8) f *= FAST ? ksh[h] : r.ks[j];
-                s[j] = (S[h][i] + dpp<kQuadSwap1>(S[h][i])) * f;
-            }
-        // Tokens past the partition end score kNegBig; only a partition's last tile has any, so the
-        // compare-and-select runs under a wave-uniform branch. (p = exp2(kNegBig - m) below is then
-        // exactly 0: m is finite, since a wave only walks tiles when its first holds a live token.)
-        if (tt + kTok > t1)
-            for (int j = 0; j < 8; ++j)
-                if (tt + kHalf * (j >> 2) + 4 * q4 + (j & 3) >= t1) s[j] = kNegBig;
-        float mx = kNegBig;
-        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, s[j]);
-        mx = max_x16_x32(mx);
-        const float mn = fmaxf(m, mx);
-        const float corr = __builtin_amdgcn_exp2f(m - mn);
-        m = mn;
-        float psum = 0.0f;
-        half8_t pb16;
+        half8_t pb16[HB];
         float pb32[F32 ? 8 : 1];
-        for (int j = 0; j < 8; ++j) {
-            const float pr = __builtin_amdgcn_exp2f(s[j] - mn);
-            psum += pr;
-            float pv = pr;
-            if constexpr (KIND == KV_I8) pv *= (FAST ? vsh[j >> 2] : r.vs[j]) * vdown;
-            if constexpr (F32) {
-                pb32[j] = hl ? 0.0f : pv;
-            } else {
-                const _Float16 hi = (_Float16)pv;
-                pb16[j] = hl ? (_Float16)(pv - (float)hi) : hi;
+        for (int hb = 0; hb < HB; ++hb) {
+            float s[8];
+            for (int h = 0; h < 2; ++h)
+                for (int i = 0; i < 4; ++i) {
+                    const int j = 4 * h + i;
+                    float f = up[hb];
+                    if constexpr (KIND == KV_I8) f *= FAST ? ksh[h] : r.ks[j];
+                    s[j] = (S[hb][h][i] + dpp<kQuadSwap1>(S[hb][h][i])) * f;
+                }
+            // Tokens past the partition end score kNegBig; only a partition's last tile has any, so the
+            // compare-and-select runs under a wave-uniform branch. (p = exp2(kNegBig - m) below is then
+            // exactly 0: m is finite, since a wave only walks tiles when its first holds a live token.)
+            if (tt + kTok > t1)
+                for (int j = 0; j < 8; ++j)
+                    if (tt + kHalf * (j >> 2) + 4 * q4 + (j & 3) >= t1) s[j] = kNegBig;
+            float mx = kNegBig;
+            for (int j = 0; j < 8; ++j) mx = fmaxf(mx, s[j]);
+            mx = max_x16_x32(mx);
+            const float mn = fmaxf(m[hb], mx);
+            const float corr = __builtin_amdgcn_exp2f(m[hb] - mn);
+            m[hb] = mn;
+            float psum = 0.0f;
+            for (int j = 0; j < 8; ++j) {
+                const float pr = __builtin_amdgcn_exp2f(s[j] - mn);
+                psum += pr;
+                float pv = pr;
+                if constexpr (KIND == KV_I8) pv *= (FAST ? vsh[j >> 2] : r.vs[j]) * vdown;
+                if constexpr (F32) {
+                    pb32[j] = hl ? 0.0f : pv;
+                } else {
+                    const _Float16 hi = (_Float16)pv;
+                    pb16[hb][j] = hl ? (_Float16)(pv - (float)hi) : hi;
+                }
             }
+            l[hb] = l[hb] * corr + psum;
+            // corr is 1 for every head whose running max did not grow: skip the no-op rescale (the
+            // accumulators may live in AGPRs, where a multiply costs two moves as well)
+            if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0)
+                for (int mb = 0; mb < NMB; ++mb) acc[hb][mb] *= corr;
         }
-        l = l * corr + psum;
-        // corr is 1 for every head whose running max did not grow: skip the no-op rescale (the
-        // accumulators may live in AGPRs, where a multiply costs two moves as well)
-        if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0)
-            for (int mb = 0; mb < NMB; ++mb) acc[mb] *= corr;
         // LDS ops of one wave execute in order; the fence keeps the compiler from moving the V^T
         // reads above the stores.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -784,7 +807,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                 for (int u = 0; u < 8; ++u) {
                     const int t = 16 * (u >> 2) + 4 * q4 + (u & 3);
                     const float a = *reinterpret_cast<const float*>(vt + t * D * 4 + 16 * ((d >> 2) ^ T::swz(t)) + 4 * (d & 3));
-                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, pb32[u], acc[mb], 0, 0, 0);
+                    acc[0][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, pb32[u], acc[0][mb], 0, 0, 0);
                 }
             } else if constexpr (KIND == KV_F16) {
                 // two reads: tokens 4 q4 + k, then 16 + 4 q4 + k (k < 4), of column d
@@ -794,13 +817,16 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                 const fp16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
                     (lds_fp16x4_t*)(vt + t1 * D * 2 + 16 * (ch ^ T::vswz(t1)) + off));
                 const half8_t a = __builtin_bit_cast(half8_t, (fp16x8_t){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-                acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb16, acc[mb], 0, 0, 0);
+                for (int hb = 0; hb < HB; ++hb)
+                    acc[hb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb16[hb], acc[hb][mb], 0, 0, 0);
             } else {
                 // one read: the 8 tokens of column d as bytes, widened to exact fp16
                 const int k = c >> 1, t = (k < 4 ? 0 : 12) + 4 * q4 + k;
                 const i32x2_t x = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
                     (lds_i32x2_t*)(vt + t * D + 16 * (mb ^ T::vswz(t)) + 8 * (c & 1)));
-                acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(x[0], x[1]), pb16, acc[mb], 0, 0, 0);
+                const half8_t a = i8x8_to_half8(x[0], x[1]);
+                for (int hb = 0; hb < HB; ++hb)
+                    acc[hb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb16[hb], acc[hb][mb], 0, 0, 0);
             }
         }
         // the next store_v overwrites the tile: keep it after these reads
@@ -827,17 +853,20 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // `live`: false writes an empty state (a wave with no tile in that partition).
     auto state_to_lds = [&](float* dst, float2* dml, bool live) {
         const float vupf = KIND == KV_I8 ? ldexpf(1.0f, ve) : 1.0f;
-        const float lsum = sum_x16_x32(l);
-        for (int mb = 0; mb < NMB; ++mb) {
-            float4 o4;  // high + low columns
-            o4.x = (acc[mb][0] + dpp<kQuadSwap1>(acc[mb][0])) * vupf;
-            o4.y = (acc[mb][1] + dpp<kQuadSwap1>(acc[mb][1])) * vupf;
-            o4.z = (acc[mb][2] + dpp<kQuadSwap1>(acc[mb][2])) * vupf;
-            o4.w = (acc[mb][3] + dpp<kQuadSwap1>(acc[mb][3])) * vupf;
-            if (!live) o4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (hl == 0 && qcol) *reinterpret_cast<float4*>(dst + hh * D + 4 * ((4 * mb + q4) ^ (hh & 7))) = o4;
+        for (int hb = 0; hb < HB; ++hb) {
+            const int hq = 8 * hb + hh;  // the workgroup's head of this lane's column
+            const float lsum = sum_x16_x32(l[hb]);
+            for (int mb = 0; mb < NMB; ++mb) {
+                float4 o4;  // high + low columns
+                o4.x = (acc[hb][mb][0] + dpp<kQuadSwap1>(acc[hb][mb][0])) * vupf;
+                o4.y = (acc[hb][mb][1] + dpp<kQuadSwap1>(acc[hb][mb][1])) * vupf;
+                o4.z = (acc[hb][mb][2] + dpp<kQuadSwap1>(acc[hb][mb][2])) * vupf;
+                o4.w = (acc[hb][mb][3] + dpp<kQuadSwap1>(acc[hb][mb][3])) * vupf;
+                if (!live) o4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (hl == 0 && qcol[hb]) *reinterpret_cast<float4*>(dst + hq * D + 4 * ((4 * mb + q4) ^ (hq & 7))) = o4;
+            }
+            if (hl == 0 && qcol[hb] && q4 == 0) dml[hq] = live ? make_float2(m[hb], lsum) : make_float2(kNegBig, 0.0f);
         }
-        if (hl == 0 && qcol && q4 == 0) dml[hh] = live ? make_float2(m, lsum) : make_float2(kNegBig, 0.0f);
     };
 
     // PAIR: `cur` is the partition of the range (0 or 1) the wave's state belongs to. At its first
@@ -855,9 +884,11 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
             if constexpr (PAIR && !LOADS) {
                 if (cur == 0 && it >= tpp && it < ntiles) {  // wave-uniform
                     state_to_lds(s_part[wave], s_ml2[wave], true);
-                    m = kNegBig;
-                    l = 0.0f;
-                    for (int mb = 0; mb < NMB; ++mb) acc[mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                    for (int hb = 0; hb < HB; ++hb) {
+                        m[hb] = kNegBig;
+                        l[hb] = 0.0f;
+                        for (int mb = 0; mb < NMB; ++mb) acc[hb][mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                    }
                     ve = -160;
                     vdown = 1.0f;
                     cur = 1;
@@ -903,11 +934,11 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // which writes through this XCD's L2 to the device coherence point, where the merging workgroup,
     // on whichever XCD, reads it.
     // PAIR: the same for each of the range's partitions (the first's states in s_part).
-    static_assert(QG * D / 4 <= 64 * W, "one 16-byte output chunk per thread");
+    // (one chunk per thread up to QG 8; QG 16 at head_dim 128: two)
     for (int gp = 0; gp < ng; ++gp) {  // uniform
       const bool lastp = gp == ng - 1;
-      if (threadIdx.x < NQ * D / 4) {
-        const int eh = threadIdx.x / (D / 4), ed = threadIdx.x % (D / 4);
+      for (int ec = threadIdx.x; ec < NQ * D / 4; ec += 64 * W) {
+        const int eh = ec / (D / 4), ed = ec % (D / 4);
         auto wml = [&](int w) { return lastp ? s_ml[w][eh] : s_ml2[PAIR ? w : 0][eh]; };
         auto wacc = [&](int w) {
             return lastp ? reinterpret_cast<const float*>(s_v[w]) : &s_part[PAIR ? w : 0][0];
@@ -978,28 +1009,28 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // partitions, it issues its rows of the first kPre partitions at once, together with the
     // (m_i, l_i) of all partitions into LDS (the V tiles are free again); then w_i replaces l_i;
     // then the sums, in partition order, with the partitions past kPre in batches of kBatch.
-    static_assert(sizeof(s_v) / sizeof(float2) == fused_merge_slots(KIND, D), "merge staging size");
+    static_assert(sizeof(s_v) / sizeof(float2) >= fused_merge_slots(KIND, D), "merge staging size");
     constexpr int kPre = 16, kBatch = 8;
     float2* s_pml = reinterpret_cast<float2*>(&s_v[0][0]);  // [QG][nparts]
     const size_t gbase = ((size_t)b * H + h0) * p.max_parts;  // first slot of head h0
     const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(
         p.part_out + gbase * D, (short)0, NQ * p.max_parts * D * 4, 0x00020000);
-    const int e = threadIdx.x, eh = e / (D / 4), ed = e % (D / 4);
-    const bool owner = e < NQ * D / 4;
-    auto row = [&](int i) {  // partition i's chunk of this thread (zeros past the group's slots)
+    // Chunk ec of the group's output is head ec / (D / 4), columns 4 (ec % (D / 4)) + 0..3. A thread
+    // owns chunks threadIdx.x + k * 64 W: one up to QG 8, two at QG 16 (head_dim 128).
+    auto row = [&](int ec, int i) {  // partition i's part of chunk ec (zeros past the group's slots)
+        const int eh = ec / (D / 4), ed = ec % (D / 4);
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                               rpo, ((eh * p.max_parts + i) * D + 4 * ed) * 4, 0, kScopeAgent));
     };
-    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float L = 0.0f;
-    auto add = [&](float wt, const float4& v) {
+    auto add = [](float4& o, float& L, float wt, const float4& v) {
         L += wt;
         o.x = __builtin_fmaf(wt, v.x, o.x);
         o.y = __builtin_fmaf(wt, v.y, o.y);
         o.z = __builtin_fmaf(wt, v.z, o.z);
         o.w = __builtin_fmaf(wt, v.w, o.w);
     };
-    auto write_out = [&]() {
+    auto write_out = [&](int ec, const float4& o, float L) {
+        const int eh = ec / (D / 4), ed = ec % (D / 4);
         *reinterpret_cast<float4*>(p.out + ((size_t)b * H + h0 + eh) * D + 4 * ed) =
             make_float4(o.x / L, o.y / L, o.z / L, o.w / L);
     };
@@ -1007,21 +1038,23 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         // Up to kPre partitions (every BASELINE configuration): each owner reads its head's (m_i, l_i)
         // straight from the workspace together with its rows, so the merge is one round trip with
         // no barrier. Same weights, same order as below.
-        if (owner) {
+        for (int ec = threadIdx.x; ec < NQ * D / 4; ec += 64 * W) {
             float4 pre[kPre];
             float2 ml[kPre];
-            const size_t mslot = gbase + (size_t)eh * p.max_parts;
+            const size_t mslot = gbase + (size_t)(ec / (D / 4)) * p.max_parts;
             for (int j = 0; j < kPre; ++j)
                 if (j < nparts) {
-                    pre[j] = row(j);
+                    pre[j] = row(ec, j);
                     ml[j] = make_float2(load_agent(&p.part_ml[mslot + j].x), load_agent(&p.part_ml[mslot + j].y));
                 }
             float M = kNegBig;
             for (int j = 0; j < kPre; ++j)
                 if (j < nparts) M = fmaxf(M, ml[j].x);
+            float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float L = 0.0f;
             for (int j = 0; j < kPre; ++j)
-                if (j < nparts) add(partition_weight(ml[j].x, ml[j].y, M), pre[j]);
-            write_out();
+                if (j < nparts) add(o, L, partition_weight(ml[j].x, ml[j].y, M), pre[j]);
+            write_out(ec, o, L);
         }
         if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef KVB_WG_TIMESTAMPS
@@ -1029,30 +1062,38 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
 #endif
         return;
     }
-    float4 pre[kPre];
-    for (int j = 0; j < kPre; ++j) pre[j] = row(j);
-    for (int x = threadIdx.x; x < NQ * nparts; x += 64 * W) {
-        const size_t slot = gbase + (size_t)(x / nparts) * p.max_parts + x % nparts;
-        s_pml[x] = make_float2(load_agent(&p.part_ml[slot].x), load_agent(&p.part_ml[slot].y));
-    }
-    __syncthreads();
-    for (int x = threadIdx.x; x < NQ * nparts; x += 64 * W) {
-        const float2* mrow = s_pml + (x / nparts) * nparts;
-        float M = kNegBig;
-        for (int i = 0; i < nparts; ++i) M = fmaxf(M, mrow[i].x);
-        s_pml[x].y = partition_weight(s_pml[x].x, s_pml[x].y, M);
-    }
-    __syncthreads();
-    if (owner) {
-        const float2* wrow = s_pml + eh * nparts;
-        for (int j = 0; j < kPre; ++j) add(wrow[j].y, pre[j]);
-        for (int i0 = kPre; i0 < nparts; i0 += kBatch) {
-            float4 v[kBatch];
-            for (int j = 0; j < kBatch; ++j) v[j] = row(i0 + j);
-            for (int j = 0; j < kBatch; ++j)
-                if (i0 + j < nparts) add(wrow[i0 + j].y, v[j]);
+    // More than kPre partitions: one chunk per thread, so QG <= 8 (the host leaves a QG 16 group
+    // with more than kPre partitions to paged_reduce).
+    if constexpr (QG <= 8) {
+        const int ec = threadIdx.x;
+        const bool owner = ec < NQ * D / 4;
+        float4 pre[kPre];
+        for (int j = 0; j < kPre; ++j) pre[j] = row(ec, j);
+        for (int x = threadIdx.x; x < NQ * nparts; x += 64 * W) {
+            const size_t slot = gbase + (size_t)(x / nparts) * p.max_parts + x % nparts;
+            s_pml[x] = make_float2(load_agent(&p.part_ml[slot].x), load_agent(&p.part_ml[slot].y));
         }
-        write_out();
+        __syncthreads();
+        for (int x = threadIdx.x; x < NQ * nparts; x += 64 * W) {
+            const float2* mrow = s_pml + (x / nparts) * nparts;
+            float M = kNegBig;
+            for (int i = 0; i < nparts; ++i) M = fmaxf(M, mrow[i].x);
+            s_pml[x].y = partition_weight(s_pml[x].x, s_pml[x].y, M);
+        }
+        __syncthreads();
+        if (owner) {
+            const float2* wrow = s_pml + (ec / (D / 4)) * nparts;
+            float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float L = 0.0f;
+            for (int j = 0; j < kPre; ++j) add(o, L, wrow[j].y, pre[j]);
+            for (int i0 = kPre; i0 < nparts; i0 += kBatch) {
+                float4 v[kBatch];
+                for (int j = 0; j < kBatch; ++j) v[j] = row(ec, i0 + j);
+                for (int j = 0; j < kBatch; ++j)
+                    if (i0 + j < nparts) add(o, L, wrow[i0 + j].y, v[j]);
+            }
+            write_out(ec, o, L);
+        }
     }
     if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef KVB_WG_TIMESTAMPS
@@ -1148,6 +1189,11 @@ hipError_t launch_for_dim(int qg, bool fast, const DecodeParams& p, int batch, h
                            : launch_qg<KIND, D, 8, true>(fast, p, batch, s, m);
         case 8: return sib ? launch_qg<KIND, D, 8, false, true>(fast, p, batch, s, m)
                            : launch_qg<KIND, D, 8, false>(fast, p, batch, s, m);
+        case 16:
+            if constexpr (KIND == KV_F16)
+                return sib ? launch_qg<KIND, D, 16, false, true>(fast, p, batch, s, m)
+                           : launch_qg<KIND, D, 16, false>(fast, p, batch, s, m);
+            return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }

@@ -211,7 +211,7 @@ int validate_paged(const kvb_paged_args* a) {
 }
 
 int query_heads_per_group(const kvb_paged_args* a) {
-    return kvb_heads_per_workgroup(a->num_heads, a->num_kv_heads, a->share_kv);
+    return kvb_heads_per_workgroup(a->num_heads, a->num_kv_heads, a->kv_type, a->share_kv);
 }
 
 // Grows the fused-merge counters to B * H ints, zeroed (the kernel leaves them at 0).
@@ -280,8 +280,10 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     p.batch = a->batch;
     p.ragged_items = ragged_items(a, part);
     p.loads_only = loads_only;
-    // fused merge when the group's partition (m, l) pairs fit its LDS staging
+    // fused merge when the group's partition (m, l) pairs fit its LDS staging; 16 heads per
+    // workgroup merge in the one-round-trip form only (at most 16 partitions)
     if (fused && qg * p.max_parts > kvbk::fused_merge_slots(a->kv_type, a->head_dim)) fused = false;
+    if (fused && qg > 8 && p.max_parts > 16) fused = false;
     if (fused) {
         p.out = a->out;
         if (counters) p.counters = counters;
@@ -431,10 +433,14 @@ int kvb_auto_part_tokens(int batch, int num_kv_heads, int max_len) {
     return part;
 }
 
-int kvb_heads_per_workgroup(int num_heads, int num_kv_heads, int share_kv) {
+int kvb_heads_per_workgroup(int num_heads, int num_kv_heads, int kv_type, int share_kv) {
     if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0) return -1;
+    if (kv_type != KVB_KV_F32 && kv_type != KVB_KV_F16 && kv_type != KVB_KV_I8) return -1;
     if (!share_kv) return 1;
     const int group = num_heads / num_kv_heads;
+    // two blocks of 8 heads: fp16 only. int8 (whose arithmetic per tile is already close to its
+    // loads) and fp32 (whose q operands are twice fp16's) run workgroups of 8.
+    if (group % 16 == 0 && kv_type == KVB_KV_F16) return 16;
     for (int g = 8; g > 1; --g)
         if (group % g == 0) return g;
     return 1;

@@ -7,8 +7,9 @@ MFMA columns past those heads stay idle. Checked for every storage type:
   workgroup), the ragged grid, and a layout whose page is not a tile multiple;
 - the fused step against the two-kernel form, bit for bit;
 - every workspace slot against the oracle's partition state;
-- groups past 8, whose KV heads have several workgroups (placed on one XCD and reading with ordinary
-  loads): each workgroup's heads bit for bit against a group-8 run of the same heads."""
+- groups of 16: each block of 8 heads (of the one f16 workgroup, or of the two f32 or i8
+  workgroups, which run on one XCD and read with ordinary loads) bit for bit against a group-8 run
+  of the same heads."""
 import numpy as np
 import pytest
 
@@ -17,7 +18,7 @@ from conftest import progress
 
 pytestmark = pytest.mark.gpu
 
-# (B, H, Hkv, D) -> query heads per workgroup
+# (B, H, Hkv, D) -> query heads per workgroup (f16; f32 and i8 caches take at most 8)
 SHAPES = [
     ((2, 24, 8, 128), 3),   # the 4-head build, one column pair idle
     ((2, 10, 2, 64), 5),    # the 8-head build from here on
@@ -26,8 +27,9 @@ SHAPES = [
     ((1, 24, 2, 128), 6),   # group 12: two workgroups per KV head
     ((1, 28, 2, 64), 7),    # group 14: two workgroups per KV head
     ((1, 18, 2, 64), 3),    # group 9: three workgroups of 3 per KV head
-    ((1, 32, 2, 128), 8),   # group 16: two workgroups of 8
-    ((1, 64, 2, 128), 8),   # group 32: four workgroups of 8
+    ((1, 32, 2, 128), 16),  # group 16: one workgroup of two 8-head blocks (f32, i8: two of 8)
+    ((1, 64, 2, 128), 16),  # group 32: two workgroups of 16 (f32, i8: four of 8)
+    ((2, 32, 1, 64), 16),   # group 32, one KV head, head_dim 64
 ]
 IDS = [f"H{s[1]}-Hkv{s[2]}-D{s[3]}" for s, _ in SHAPES]
 
@@ -57,7 +59,8 @@ def pair_restored(gpu):
 def test_groups_match_the_oracle(pair_restored, oracle, shape, qg, kv):
     kvb = pair_restored
     s = kvb.Shape(*shape)
-    assert kvb.heads_per_workgroup(s) == qg
+    qg = qg if kv == "f16" else min(qg, 8)
+    assert kvb.heads_per_workgroup(s, kv) == qg
     for kind, page, part in LAYOUTS:
         w = kvb.Workload(s, kv, lengths(kind, s.batch), seed=qg * 97 + page, varied=(kv == "i8"))
         c = kvb.PagedCache(w, page, 13 * page + qg, pool_factor=1.5, poison=True)
@@ -82,7 +85,7 @@ def test_groups_match_the_oracle(pair_restored, oracle, shape, qg, kv):
 
 
 @pytest.mark.parametrize("kv", ["f16", "i8"])
-@pytest.mark.parametrize("shape,qg", [SHAPES[0], SHAPES[3], SHAPES[5]], ids=[IDS[0], IDS[3], IDS[5]])
+@pytest.mark.parametrize("shape,qg", [SHAPES[i] for i in (0, 3, 5, 7, 9)], ids=[IDS[i] for i in (0, 3, 5, 7, 9)])
 def test_groups_workspace_slots(gpu, oracle, shape, qg, kv):
     """Every (sequence, head, partition) slot: the oracle's (m, l, o) where the partition holds
     tokens, untouched (NaN) elsewhere. A head's slot depends on its own index only, so a workgroup
@@ -127,9 +130,10 @@ def test_groups_workspace_slots(gpu, oracle, shape, qg, kv):
 @pytest.mark.parametrize("lens,part", [([1000, 1000], 256), ([1000, 1000], 128), ([777, 65, 300, 1], 128),
                                        ([4096, 4096, 4096, 4096], 512), ([500, 300, 120], 160)])
 def test_sibling_workgroups_give_group8_bits(gpu, kv, lens, part):
-    """Group 16 runs two workgroups of 8 heads per KV head. Each gives the same bits as a group-8
-    run over the same K/V with its 8 heads as the group, with the sibling order (when the
-    (KV head, sequence, partition) units fill blocks of 8) and without it."""
+    """Group 16: f16 runs one workgroup of two 8-head blocks per KV head, f32 and i8 two workgroups
+    of 8 (with the sibling order when the (KV head, sequence, partition) units fill blocks of 8, else
+    without it). Each block of 8 heads gives the same bits as a group-8 run over the same K/V with
+    those heads as the group."""
     kvb = gpu
     B = len(lens)
     w16 = kvb.Workload(kvb.Shape(B, 32, 2, 128), kv, lens, seed=len(lens) * 31 + part)
@@ -154,3 +158,24 @@ def test_sibling_workgroups_give_group8_bits(gpu, kv, lens, part):
         d8.free()
         assert np.array_equal(out16[:, heads].view(np.uint32), out8.view(np.uint32)), half
     progress(f"[groups] group 16 = 2 x group 8 bits, {kv} lens {lens} part {part} ({units} units)")
+
+
+@pytest.mark.parametrize("kv", ["f16"])
+def test_sixteen_heads_past_sixteen_partitions(gpu, oracle, kv):
+    """A 16-head workgroup merges at most 16 partitions in the fused step; with more, the step is
+    paged_decode then paged_reduce. Against the oracle, and fused (requested) equal to two-kernel."""
+    kvb = gpu
+    w = kvb.Workload(kvb.Shape(2, 32, 2, 128), kv, [1000, 333], seed=77, varied=(kv == "i8"))
+    c = kvb.PagedCache(w, 16, 9, pool_factor=1.5, poison=True)
+    for part in (32, 64):  # 32 and 16 partitions
+        dev = kvb.DeviceCase(w, c)
+        dev.out.fill(0xFF)
+        dev.run(part)
+        fused = dev.output().copy()
+        dev.out.fill(0xFF)
+        dev.run_split(part)
+        split = dev.output().copy()
+        dev.free()
+        assert np.array_equal(fused.view(np.uint32), split.view(np.uint32)), part
+        err = pb.check_output(kvb, oracle, w, c, fused)
+        progress(f"[groups] 16 heads, {kv}, part {part}: max err {err:.3g}")

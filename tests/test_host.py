@@ -217,21 +217,35 @@ def test_c_abi_auto_part_tokens_thresholds(kvb, oracle):
 
 
 def test_heads_per_workgroup(kvb):
-    """kvb_heads_per_workgroup: the largest divisor of the group that is at most 8 (one workgroup
-    reads each K/V page for that many query heads), 1 without share_kv, -1 for shapes the decode
-    refuses. Spot values, then every group to 64 against a brute-force search over 8..1."""
+    """kvb_heads_per_workgroup: one workgroup reads each K/V page for this many query heads. 16
+    for a group that is a multiple of 16 with an f16 cache (two blocks of 8 heads), else the
+    largest divisor of the group that is at most 8; 1 without share_kv; -1 for shapes the decode
+    refuses. Spot values, then every group to 64 against a brute-force search."""
     spot = {1: 1, 2: 2, 3: 3, 4: 4, 5: 5, 6: 6, 7: 7, 8: 8, 9: 3, 10: 5, 11: 1, 12: 6, 13: 1, 14: 7, 15: 5,
             16: 8, 18: 6, 20: 5, 21: 7, 24: 8, 28: 7, 40: 8, 64: 8}
+    F32, F16, I8 = kvb.KV_F32, kvb.KV_F16, kvb.KV_I8
     for g, want in spot.items():
-        assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, 1) == want, g
-        assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, 0) == 1
+        assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, F32, 1) == want, g
+        want16 = 16 if g % 16 == 0 else want
+        assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, F16, 1) == want16, g
+        assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, I8, 1) == want, g
+        for kv in (F32, F16, I8):
+            assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, kv, 0) == 1
     for g in range(1, 65):
-        got = kvb.hip.kvb_heads_per_workgroup(g * 2, 2, 1)
-        assert g % got == 0 and got <= 8
-        assert all(g % d != 0 for d in range(got + 1, 9)), g
+        for kv in (F32, F16):
+            got = kvb.hip.kvb_heads_per_workgroup(g * 2, 2, kv, 1)
+            if kv == F16 and g % 16 == 0:
+                assert got == 16
+                continue
+            assert g % got == 0 and got <= 8
+            assert all(g % d != 0 for d in range(got + 1, 9)), g
     for h, hkv in ((8, 0), (0, 8), (12, 8), (-8, 8), (8, -2)):
-        assert kvb.hip.kvb_heads_per_workgroup(h, hkv, 1) == -1, (h, hkv)
+        assert kvb.hip.kvb_heads_per_workgroup(h, hkv, F16, 1) == -1, (h, hkv)
+    assert kvb.hip.kvb_heads_per_workgroup(16, 8, 3, 1) == -1
     assert kvb.heads_per_workgroup(kvb.Shape(2, 56, 8, 128)) == 7
+    assert kvb.heads_per_workgroup(kvb.Shape(1, 16, 1, 128), "f32") == 8
+    assert kvb.heads_per_workgroup(kvb.Shape(1, 16, 1, 128), "i8") == 8
+    assert kvb.heads_per_workgroup(kvb.Shape(1, 16, 1, 128), "f16") == 16
 
 
 def test_partition_policy_counts_live_heads(kvb):
