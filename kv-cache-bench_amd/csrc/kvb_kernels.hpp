@@ -95,7 +95,14 @@ struct DecodeParams {
     // kernels only (the others serve QG heads). Last, so that it leaves the other fields' offsets
     // in the kernel arguments as they were.
     int qg;
+    // Nonzero (any-page path only, page_size or part_tokens not a multiple of kTile): a workgroup's
+    // range touches at most kTableStage blocks, so the STAGE kernel copies their ids into LDS.
+    int table_in_lds;
 };
+
+// Block ids the any-page kernel stages in LDS per workgroup (16 KB): a 4096-token partition at any
+// page size, page 1 included.
+constexpr int kTableStage = 4096;
 
 // Blocks of one partition that paged_decode holds in lanes: one per lane of one VGPR (and, for int8,
 // one VGPR each for the K and V scales). With more, it reads the block table per tile instead.

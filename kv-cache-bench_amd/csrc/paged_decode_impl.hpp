@@ -326,7 +326,7 @@ __device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int bat
 // a workgroup of its own (part_tokens is a multiple of 32 * waves), and a wave starts its second
 // partition from a fresh state, so every partition gets the same bits either way.
 template <int KIND, int D, int QG, bool FAST, bool LOADS = false, bool PAIR = false, bool PART = false,
-          bool SHARE = false>
+          bool SHARE = false, bool STAGE = false>
 __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(QG > 8 ? 1 : KIND == KV_I8 && FAST && !LOADS && !PAIR && QG > 1 ? 3 : 2))) void paged_decode_kernel(DecodeParams p) {
     using T = KvT<KIND, D>;
     using R = TileRegs<KIND, D>;
@@ -430,6 +430,23 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // caches an HBM round trip per tile (c3 int8 on MI355X: 48.3 us per step that way, 46.5 us with
     // the scales in lanes).
     const const_i32 bt = (const_i32)p.block_table + (size_t)b * p.max_blocks;
+    // STAGE (the any-page path): each lane finds the block of its own rows, so its lookups are
+    // vector reads, and a vector load of a block id would be waited for together with every tile
+    // still in flight (vmcnt counts in issue order), which serialises the walk. The range's block
+    // ids are copied into LDS once instead, and a lookup is an LDS read. (MI355X, c4's size with
+    // 8-token pages: see the tile walk.)
+    static_assert(!STAGE || !FAST, "STAGE is an any-page variant");
+    __shared__ int s_tab[STAGE ? kTableStage : 1];
+    const int tb0 = fast_div(t0, p.page_div);
+    if constexpr (STAGE) {
+        const int nbs = fast_div(t1 - 1, p.page_div) - tb0 + 1;  // <= kTableStage (host-checked)
+        for (int i = threadIdx.x; i < nbs; i += 64 * W) s_tab[i] = p.block_table[(size_t)b * p.max_blocks + tb0 + i];
+        __syncthreads();
+    }
+    auto block_of = [&](int bi) -> int {
+        if constexpr (STAGE) return s_tab[bi - tb0];
+        else return bt[bi];
+    };
     const const_f32 ksc = (const_f32)p.k_scale, vsc = (const_f32)p.v_scale;
     const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.k_scale), (short)0,
                                                                          0x7fffffff, 0x00020000);
@@ -504,7 +521,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                 const int tk = th + c;
                 const int tks = tk < t1 ? tk : t0;
                 const int kbi = fast_div(tks, p.page_div);
-                const int kid = bt[kbi];
+                const int kid = block_of(kbi);
                 const bool kval = tk < t1 && kid >= 0;
                 const size_t krow = ((size_t)max(kid, 0) * Hkv + kvh) * P + (tks - kbi * P);
                 const char* kb = kbase + krow * D * T::ESZ;
@@ -516,7 +533,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                     const int tv = th + i * (64 / VL) + lane / VL;
                     const int tvs = tv < t1 ? tv : t0;
                     const int vbi = fast_div(tvs, p.page_div);
-                    const int vid = bt[vbi];
+                    const int vid = block_of(vbi);
                     const bool vval = tv < t1 && vid >= 0;
                     const size_t vrow = ((size_t)max(vid, 0) * Hkv + kvh) * P + (tvs - vbi * P);
                     const uint4 x = *reinterpret_cast<const uint4*>(vbase + vrow * D * T::ESZ + (lane % VL) * 16);
@@ -526,7 +543,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                     for (int i = 0; i < 4; ++i) {  // the score-layout tokens th + 4*q4 + i of this lane
                         const int ts = th + 4 * q4 + i;
                         const int tss = ts < t1 ? ts : t0;
-                        const size_t slot = (size_t)max(bt[fast_div(tss, p.page_div)], 0) * Hkv + kvh;
+                        const size_t slot = (size_t)max(block_of(fast_div(tss, p.page_div)), 0) * Hkv + kvh;
                         r.ks[4 * h + i] = ksc[slot];
                         r.vs[4 * h + i] = vsc[slot];
                     }
@@ -1140,7 +1157,7 @@ hipError_t loads_only_lds(size_t* lds) {
     return hipSuccess;
 }
 
-template <int KIND, int D, int QG, bool FAST, bool PAIR, bool PART, bool SHARE>
+template <int KIND, int D, int QG, bool FAST, bool PAIR, bool PART, bool SHARE, bool STAGE = false>
 hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
     const int gz = PAIR ? (p.max_parts + 1) / 2 : p.max_parts;
     const dim3 grid(p.num_heads / p.qg, p.ragged_items ? p.ragged_items : batch, p.ragged_items ? 1 : gz);
@@ -1154,7 +1171,7 @@ hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Mar
                               lds, s, m, p);
         }
     } else {
-        launch_marked(paged_decode_kernel<KIND, D, QG, FAST, false, PAIR, PART, SHARE>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
+        launch_marked(paged_decode_kernel<KIND, D, QG, FAST, false, PAIR, PART, SHARE, STAGE>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
     }
     return hipGetLastError();
 }
@@ -1162,7 +1179,11 @@ hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Mar
 // Two partitions per workgroup (DecodeParams::pair): tile-aligned f16 and i8 caches, plain grid only.
 template <int KIND, int D, int QG, bool PART, bool SHARE = false>
 hipError_t launch_qg(bool fast, const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
-    if (!fast) return p.pair ? hipErrorInvalidValue : launch_one<KIND, D, QG, false, false, PART, SHARE>(p, batch, s, m);
+    if (!fast) {
+        if (p.pair) return hipErrorInvalidValue;
+        return p.table_in_lds ? launch_one<KIND, D, QG, false, false, PART, SHARE, true>(p, batch, s, m)
+                              : launch_one<KIND, D, QG, false, false, PART, SHARE>(p, batch, s, m);
+    }
     if constexpr (KIND != KV_F32) {
         if (p.pair) return p.ragged_items ? hipErrorInvalidValue : launch_one<KIND, D, QG, true, true, PART, SHARE>(p, batch, s, m);
     } else {

@@ -303,6 +303,7 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     const long long span = (p.pair ? 2LL : 1LL) * part;
     const long long nb_max = span % a->page_size == 0 ? span / a->page_size : span / a->page_size + 2;
     p.table_in_lanes = fast && nb_max <= kvbk::kLaneBlocks;
+    p.table_in_lds = !fast && nb_max <= kvbk::kTableStage;
     const kvbk::Marks dm{mk.step.start ? mk.step.start : mk.decode.start, fused ? mk.step.stop : mk.decode.stop};
     const kvbk::Marks rm{mk.reduce.start, mk.step.stop ? mk.step.stop : mk.reduce.stop};
     hipError_t e = hipSuccess;

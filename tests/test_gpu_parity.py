@@ -375,3 +375,18 @@ def test_non_finite_query_poisons_only_its_head(gpu, oracle, kv):
         keep[0, 1] = False
         assert np.abs(got[keep] - clean[keep]).max() <= tol, bad
         w.q[0, 1, 17] = 0.5
+
+
+@pytest.mark.parametrize("kv", ["f32", "f16", "i8"])
+def test_any_page_table_staged_and_not(gpu, oracle, kv):
+    """The any-page path (page or partition not a multiple of 16) copies a workgroup's block ids
+    into LDS when its range touches at most kTableStage (4096) blocks, and reads the table in
+    memory otherwise. Page 1: a 4096-token partition stages exactly 4096 ids; a 5000-token one
+    touches 5000 and does not; page 7 with a partition of 100 stages 16."""
+    kvb = gpu
+    for page, part, lens in ((1, 4096, [4096, 1000]), (1, 5000, [6000, 333]), (7, 100, [777, 50])):
+        w = kvb.Workload(kvb.Shape(len(lens), 8, 2, 64), kv, lens, seed=page * 1000 + part, varied=(kv == "i8"))
+        c = kvb.PagedCache(w, page, part + 3, pool_factor=1.25, poison=True)
+        got = run(kvb, w, c, part)
+        err = pb.check_output(kvb, oracle, w, c, got)
+        progress(f"[any-page] {kv} page {page} part {part}: max err {err:.3g}")
