@@ -13,7 +13,15 @@ Groups:
           of this build's split-K kernel (kvbo_split_decode in oracle/kvb_oracle.c, which uses the
           kernel's number formats). They are checked by tests/test_split_model.py, which is the GPU
           parity battery (tests/parity_battery.py) run on that model. No deliberately broken kernel
-          runs on a GPU (the GPU boxes forbid it), and the HIP kernel cannot run on the CPU.
+          runs on a GPU (the GPU boxes forbid it); group hip runs the kernel's own source mutated,
+          on the CPU emulation.
+  hip     mistakes planted in the shipped kernels' own source (paged_decode_impl.hpp and its
+          headers, paged_reduce, the cache writer): the arithmetic of the MFMA kernel (the q and p
+          high/low columns, the int8 q digits, the V-scale power of two, the DPP column sums), its
+          indexing (the V swizzle, rows inside a page, block ids, the tail mask, the sibling and
+          ragged work orders, pair mode) and its merges. The mutated sources are compiled for the
+          CPU emulation of gfx950 (tests/kernel_emu) and the GPU test files run on that build
+          (tests/kernel_emu/run_gpu_tests.py, stopping at the first failure). Nothing runs on a GPU.
   oracle  mistakes in the checker itself (fp64 attention, layout, quantiser, f16 rounding, RNG,
           storage-error bounds), checked by tests/test_oracle.py: the pins against the reference's
           own build, its golden vectors and closed forms.
@@ -45,8 +53,10 @@ ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)
 REFERENCE = "/root/reference"  # the reference's test programs are rebuilt from its sources there
 ORACLE_C = "oracle/kvb_oracle.c"
 RUNTIME = "kv-cache-bench_amd/csrc/runtime.hip"
+KERNEL = "kv-cache-bench_amd/csrc/paged_decode_impl.hpp"
 GROUP_TESTS = {
     "kernel": ["tests/test_split_model.py"],
+    "hip": ["tests/kernel_emu/run_gpu_tests.py"],
     "oracle": ["tests/test_oracle.py"],
     "host": ["tests/test_host.py", "tests/test_abi.py", "tests/test_cpp_programs.py"],
 }
@@ -72,6 +82,10 @@ def O(name, old, new):
 
 def H(name, path, old, new):
     return Mutant("host", name, path, old, new)
+
+
+def X(name, old, new, path=KERNEL):
+    return Mutant("hip", f"{name} [hip]", path, old, new)
 
 
 MUTANTS = [
@@ -132,6 +146,71 @@ MUTANTS = [
       "return len < 0 ? 0 : len > j->len_cap ? j->len_cap : len;", "return len;"),
     K("partition weight without l (w = exp(m - M))",
       "const float w = ml[2 * i + 1] * exp_ftz(ml[2 * i] - M);", "const float w = exp_ftz(ml[2 * i] - M);"),
+    # ---- the shipped kernels' source, run on the CPU emulation (reference: scripts/mutation.sh:50-59) ----
+    X("online-softmax rescale dropped (corr = 1)",
+      "const float corr = __builtin_amdgcn_exp2f(m[hb] - mn);", "const float corr = 1.0f;"),
+    X("softmax scale not applied", "qv[hb][j][s] * p.qscale : 0.0f;", "qv[hb][j][s] : 0.0f;"),
+    X("q loaded for the head block's first head in every column",
+      "h0 + (qcol[hb] ? 8 * hb + hh : 0)) * D;", "h0 + (qcol[hb] ? 8 * hb : 0)) * D;"),
+    X("fp16 q: low column dropped (q as one fp16 number)",
+      "aq16[hb][j][s] = hl ? lo : hi;", "aq16[hb][j][s] = hl ? (_Float16)0.0f : hi;"),
+    X("scores: the low column's DPP sum dropped",
+      "s[j] = (S[hb][h][i] + dpp<kQuadSwap1>(S[hb][h][i])) * f;", "s[j] = S[hb][h][i] * f;"),
+    X("int8 q: second digit weighted 2^-6 instead of 2^-7",
+      "const float wa = hl ? 1.0f / 128.0f : 1.0f,", "const float wa = hl ? 1.0f / 64.0f : 1.0f,"),
+    X("int8 q: third digit dropped", "wb = hl ? 0.0f : 1.0f / 16384.0f;", "wb = 0.0f;"),
+    X("int8: K scale not applied", "if constexpr (KIND == KV_I8) f *= FAST ? ksh[h] : r.ks[j];", "(void)ksh;"),
+    X("int8: scales of KV head 0 for every head (partition in lanes)",
+      "const int soff = lane < nb ? (max(blkv, 0) * Hkv + kvh) * 4 : 0;",
+      "const int soff = lane < nb ? (max(blkv, 0) * Hkv) * 4 : 0;"),
+    X("p: low fp16 column dropped (p as one fp16 number)",
+      "pb16[hb][j] = hl ? (_Float16)(pv - (float)hi) : hi;", "pb16[hb][j] = hl ? (_Float16)0.0f : hi;"),
+    X("int8: p * v_scale not normalised by the running power of two",
+      "pv *= (FAST ? vsh[j >> 2] : r.vs[j]) * vdown;", "pv *= FAST ? vsh[j >> 2] : r.vs[j];"),
+    X("int8: the V-scale power of two not undone at the end",
+      "const float vupf = KIND == KV_I8 ? ldexpf(1.0f, ve) : 1.0f;", "const float vupf = 1.0f;"),
+    X("tail mask off by one (the token at the partition end scored)",
+      "if (tt + kHalf * (j >> 2) + 4 * q4 + (j & 3) >= t1) s[j] = kNegBig;",
+      "if (tt + kHalf * (j >> 2) + 4 * q4 + (j & 3) > t1) s[j] = kNegBig;"),
+    X("V tile stored without its swizzle (read with it)", "else sch = ch ^ T::vswz(t);", "else sch = ch;"),
+    X("tile-aligned pages: K and V one row later inside the page",
+      "const size_t row0 = ((size_t)blk * Hkv + kvh) * P + off;",
+      "const size_t row0 = ((size_t)blk * Hkv + kvh) * P + off + 1;"),
+    X("tile-aligned pages: the second half tile reads the first half's rows", "off += kHalf;", "off += 0;"),
+    X("the partition's first block for every tile (block ids in lanes)",
+      "braw = lanes ? lane_block(bi - bi0) : bt[bi];", "braw = lanes ? lane_block(0) : bt[bi];"),
+    X("any page size: V one row later inside the page",
+      "* P + (tvs - vbi * P);", "* P + (tvs + 1 - vbi * P) % P;"),
+    X("wave merge weight exp(M - m) instead of exp(m - M)",
+      "const float wt = __builtin_amdgcn_exp2f(wml(w).x - M);", "const float wt = __builtin_amdgcn_exp2f(M - wml(w).x);"),
+    X("wave merge reads the other waves' rows without their swizzle",
+      "wacc(w) + eh * D + 4 * (ed ^ (eh & 7)));", "wacc(w) + eh * D + 4 * ed);"),
+    X("partition output not divided by its sum",
+      "const float4 r = make_float4(o.x / L, o.y / L, o.z / L, o.w / L);",
+      "const float4 r = make_float4(o.x, o.y, o.z, o.w);"),
+    X("fused merge counts only the full partitions",
+      "const int nparts = (len + p.part_tokens - 1) / p.part_tokens;", "const int nparts = len / p.part_tokens;"),
+    X("fused merge weighs every partition with partition 0's max",
+      "add(o, L, partition_weight(ml[j].x, ml[j].y, M), pre[j]);",
+      "add(o, L, partition_weight(ml[0].x, ml[j].y, M), pre[j]);"),
+    X("fused merge leaves its arrival counter set",
+      "        if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);",
+      ""),
+    X("partition weight without l (w = exp(m - M))",
+      "return l * __builtin_amdgcn_exp2f((m - M) * 1.4426950408889634f);",
+      "return __builtin_amdgcn_exp2f((m - M) * 1.4426950408889634f);", "kv-cache-bench_amd/csrc/kvb_kernels.hpp"),
+    X("pair mode: the second partition starts one tile late",
+      "if (cur == 0 && it >= tpp && it < ntiles)", "if (cur == 0 && it > tpp && it < ntiles)"),
+    X("sibling workgroups all take the KV head's first head block",
+      "bx = (int)((unit % XK) * S + within / 8);", "bx = (int)((unit % XK) * S);"),
+    X("ragged order: full partitions numbered from 1",
+      "r = WorkItem{64 * e + l, i - __builtin_amdgcn_readlane(excl, l)};",
+      "r = WorkItem{64 * e + l, i + 1 - __builtin_amdgcn_readlane(excl, l)};"),
+    X("paged_reduce reads partition 0's rows for every partition",
+      "acc = __builtin_fmaf(w, p.part_out[(base + i) * D + d], acc);",
+      "acc = __builtin_fmaf(w, p.part_out[base * D + d], acc);", "kv-cache-bench_amd/csrc/kernels_misc.hip"),
+    X("cache writer: int8 quantiser truncates",
+      "__builtin_rintf(x / scale)", "truncf(x / scale)", "kv-cache-bench_amd/csrc/cache_writer.hip"),
     # ---- the checker ----
     O("fp64 reference has no case for an empty sequence (scripts/mutation.sh:36)",
       "len ? (float)(acc[d] / sum) : 0.0f", "(float)(acc[d] / sum)"),
@@ -251,7 +330,13 @@ def prepare(m: Mutant, work: str) -> tuple[dict, str]:
     """Copies what the mutant's group builds, applies the mutant and builds. Returns the
     environment for the test run and the build log."""
     env = dict(os.environ)
-    if m.group in ("kernel", "oracle"):
+    if m.group == "hip":
+        skip = shutil.ignore_patterns("__pycache__")
+        for d in ("kv-cache-bench_amd/csrc", "kv-cache-bench_amd/host", "include", "tests/kernel_emu"):
+            _copy(d, work, skip)  # (with the emulated build's objects: only what the mutant touches rebuilds)
+        cmd = ["make", "-C", os.path.join(work, "tests", "kernel_emu"), "-j8", "libs"]
+        env["KVB_EMU_BUILD"] = os.path.join(work, "tests", "kernel_emu", "build")
+    elif m.group in ("kernel", "oracle"):
         for f in ("oracle/Makefile", "oracle/kvb_oracle.h", ORACLE_C):
             _copy(f, work)
         cmd = ["make", "-C", os.path.join(work, "oracle"), "all"]
@@ -283,10 +368,14 @@ def prepare(m: Mutant, work: str) -> tuple[dict, str]:
 
 def run_tests(m: Mutant, env: dict, fail_fast=False):
     """(caught, summary). Runs the group's tests in a child process group of its own."""
-    cmd = [sys.executable, "-m", "pytest", *GROUP_TESTS[m.group], "-q", "-m", "not gpu", "-rf",
-           "-p", "no:cacheprovider", "-o", "console_output_style=classic"]
-    if fail_fast:
-        cmd.append("-x")
+    if m.group == "hip":  # the GPU test files on the mutated kernels' CPU emulation, to the first failure
+        cmd = [sys.executable, os.path.join(ROOT, GROUP_TESTS["hip"][0]), "--build-dir", env["KVB_EMU_BUILD"], "-x",
+               "-rf", "-o", "console_output_style=classic"]
+    else:
+        cmd = [sys.executable, "-m", "pytest", *GROUP_TESTS[m.group], "-q", "-m", "not gpu", "-rf",
+               "-p", "no:cacheprovider", "-o", "console_output_style=classic"]
+        if fail_fast:
+            cmd.append("-x")
     p = subprocess.Popen(cmd, cwd=ROOT, env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
                          start_new_session=True)
     try:
@@ -303,7 +392,8 @@ def run_tests(m: Mutant, env: dict, fail_fast=False):
     failed = [f.replace("tests/", "", 1) for f in failed]
     counts = re.findall(r"(\d+) (passed|failed|error)", tail)
     summary = ", ".join(f"{n} {w}" for n, w in counts) or tail
-    if p.returncode == 1:
+    # (pytest-xdist stopping at the first failure exits with 2, "interrupted", after its failures)
+    if p.returncode == 1 or (p.returncode == 2 and any(w == "failed" and int(n) > 0 for n, w in counts)):
         shown = "; ".join(failed[:3]) + (f"; +{len(failed) - 3} more" if len(failed) > 3 else "")
         return True, f"{summary}: {shown}"
     if p.returncode == 0:
