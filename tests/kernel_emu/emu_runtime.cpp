@@ -7,6 +7,17 @@
 #include <sys/mman.h>
 #include <unistd.h>
 
+// Under AddressSanitizer (make -C tests/kernel_emu asan): every plain load and store of the
+// kernels is checked too, and the fiber switches are announced to it so that each fiber's stack is
+// its own.
+#if defined(__has_feature)
+#if __has_feature(address_sanitizer)
+#define KVBEMU_ASAN 1
+#include <sanitizer/asan_interface.h>
+#include <sanitizer/common_interface_defs.h>
+#endif
+#endif
+
 #include <chrono>
 #include <cstdarg>
 #include <map>
@@ -65,6 +76,37 @@ hipError_t g_last_err = hipSuccess;
 std::vector<Fiber> g_fibers;
 std::vector<char*> g_stacks;
 std::map<uintptr_t, size_t> g_allocs;  // base -> bytes: hipMalloc and registered symbols
+#ifdef KVBEMU_ASAN
+const void* g_sched_bottom = nullptr;  // the scheduler's stack, as AddressSanitizer reports it
+size_t g_sched_size = 0;
+#endif
+
+// The scheduler resumes fiber f, until it yields or ends.
+void switch_to_fiber(Fiber& f) {
+#ifdef KVBEMU_ASAN
+    void* fake = nullptr;
+    __sanitizer_start_switch_fiber(&fake, f.stack, kStackBytes);
+#endif
+    kvbemu_switch(&g_sched_sp, f.sp);
+#ifdef KVBEMU_ASAN
+    __sanitizer_finish_switch_fiber(fake, nullptr, nullptr);
+#endif
+}
+
+// The running fiber hands control back to the scheduler; `ending`: it will never be resumed.
+void switch_to_scheduler(bool ending) {
+    Fiber* me = g_cur;
+#ifdef KVBEMU_ASAN
+    void* fake = nullptr;
+    __sanitizer_start_switch_fiber(ending ? nullptr : &fake, g_sched_bottom, g_sched_size);
+#else
+    (void)ending;
+#endif
+    kvbemu_switch(&me->sp, g_sched_sp);
+#ifdef KVBEMU_ASAN
+    __sanitizer_finish_switch_fiber(fake, &g_sched_bottom, &g_sched_size);
+#endif
+}
 
 char* new_stack() {
     const long page = sysconf(_SC_PAGESIZE);
@@ -83,6 +125,9 @@ char* new_stack() {
 // word, six registers, the return address), then a null return address for fiber_main so that it
 // is entered with the stack alignment of a call.
 void* init_context(char* stack) {
+#ifdef KVBEMU_ASAN
+    __asan_unpoison_memory_region(stack, kStackBytes);  // (frames of an abandoned fiber left poison)
+#endif
     uintptr_t top = reinterpret_cast<uintptr_t>(stack + kStackBytes) & ~uintptr_t(15);
     uint64_t* sp = reinterpret_cast<uint64_t*>(top - 72);
     sp[0] = 0x1F80ull | (0x037Full << 32);  // MXCSR default, x87 control word default
@@ -93,6 +138,9 @@ void* init_context(char* stack) {
 }
 
 void fiber_main() {
+#ifdef KVBEMU_ASAN
+    __sanitizer_finish_switch_fiber(nullptr, &g_sched_bottom, &g_sched_size);
+#endif
     (*g_grp->body)();
     Fiber* me = g_cur;
     Group& g = *g_grp;
@@ -107,7 +155,7 @@ void fiber_main() {
         g.bar_arrived = 0;
         ++g.bar_gen;
     }
-    kvbemu_switch(&me->sp, g_sched_sp);
+    switch_to_scheduler(true);
     __builtin_unreachable();  // a finished fiber is never resumed
 }
 
@@ -135,11 +183,11 @@ void fail(const char* fmt, ...) {
     std::fprintf(stderr, "kvbemu: %s\n", g_msg.c_str());
     if (!g_cur || !g_sched_sp) std::abort();  // outside a launch: nothing to return to
     g_failed = true;
-    kvbemu_switch(&g_cur->sp, g_sched_sp);
+    switch_to_scheduler(true);
     __builtin_unreachable();  // the failed launch's fibers are abandoned, never resumed
 }
 
-void yield() { kvbemu_switch(&g_cur->sp, g_sched_sp); }
+void yield() { switch_to_scheduler(false); }
 
 void syncthreads() {
     Group& g = *g_grp;
@@ -219,7 +267,7 @@ hipError_t launch(dim3 grid, dim3 block, const std::function<void()>& body) {
                     for (Fiber& f : g_fibers) {
                         if (f.done) continue;
                         g_cur = &f;
-                        kvbemu_switch(&g_sched_sp, f.sp);
+                        switch_to_fiber(f);
                         if (g_failed) break;
                     }
                     if (!g_failed && grp.live > 0 && grp.progress == before) {

@@ -9,8 +9,12 @@ hardware or need the HIP runtime itself: full-size configurations (hours on the 
 4 GiB read probe, graph capture, stream switching through libamdhip64, and the C++ programs and
 benchmarks that load the GPU build.
 
+With --asan the libraries are the AddressSanitizer build (make -C tests/kernel_emu asan), so every
+plain load and store the kernels make is checked against its allocation, in addition to the
+emulation's own checks of buffer accesses.
+
 Usage:
-  python tests/kernel_emu/run_gpu_tests.py [--build-dir DIR] [--all] [-x] [-n WORKERS] [pytest args...]
+  python tests/kernel_emu/run_gpu_tests.py [--build-dir DIR] [--asan] [--all] [-x] [-n WORKERS] [pytest args...]
 --all adds the slow cases (about 25 minutes of CPU time); the default set takes about 6 minutes of
 CPU time, spread over the workers.
 """
@@ -24,9 +28,12 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 BUILD = os.path.join(HERE, "build")
+ASAN_BUILD = os.path.join(HERE, "build-asan")
+CXX = "/opt/rocm/lib/llvm/bin/clang++"
 
 FILES = ["tests/test_gpu_parity.py", "tests/test_gpu_groups.py", "tests/test_gpu_pair.py",
-         "tests/test_gpu_writer.py", "tests/test_zz_no_alloc.py"]
+         "tests/test_gpu_writer.py", "tests/test_zz_no_alloc.py",
+         "tests/kernel_emu/cases_emu_only.py"]  # (the last: lengths the host did not check)
 # hardware measurements, or calls into the HIP runtime itself
 HARDWARE = "not full_size and not stream_switch and not read_bandwidth"
 # slow on the emulation (a minute or more each); --all runs them
@@ -52,16 +59,24 @@ def command(build_dir: str, all_cases: bool, stop_first: bool, workers: int, ext
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--build-dir", default=BUILD, help="the emulated build (default: tests/kernel_emu/build)")
+    ap.add_argument("--build-dir", help="the emulated build (default: tests/kernel_emu/build, or build-asan)")
+    ap.add_argument("--asan", action="store_true", help="the AddressSanitizer build, with its runtime preloaded")
     ap.add_argument("--all", action="store_true", help="include the slow cases")
     ap.add_argument("-x", action="store_true", help="stop at the first failure")
     ap.add_argument("-n", type=int, default=min(8, os.cpu_count() or 1), help="pytest-xdist workers")
     args, extra = ap.parse_known_args(argv)
+    args.build_dir = args.build_dir or (ASAN_BUILD if args.asan else BUILD)
     for lib in ("libkvb_hip.so", "libkvb_host.so"):
         if not os.path.exists(os.path.join(args.build_dir, lib)):
             print(f"{args.build_dir}/{lib} is not built: make -C tests/kernel_emu", file=sys.stderr)
             return 2
     env = dict(os.environ, KVB_BUILD_DIR=os.path.abspath(args.build_dir))
+    if args.asan:
+        runtime = subprocess.run([CXX, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True,
+                                 text=True, check=True).stdout.strip()
+        env["LD_PRELOAD"] = runtime
+        # (Python and numpy are not instrumented: only the emulated libraries' accesses are checked)
+        env["ASAN_OPTIONS"] = "detect_leaks=0:abort_on_error=1:allocator_may_return_null=1"
     return subprocess.run(command(args.build_dir, args.all, args.x, args.n, extra), cwd=ROOT, env=env).returncode
 
 

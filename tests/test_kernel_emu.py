@@ -4,6 +4,10 @@ range-checked buffer loads) into a libkvb_hip.so with the same C ABI, and the GP
 it unchanged (tests/kernel_emu/run_gpu_tests.py). The mutation harness plants kernel mistakes in
 that source and checks them the same way (tests/mutation/mutate.py, group hip).
 
+Under AddressSanitizer (make -C tests/kernel_emu asan) every plain load and store of the kernels is
+checked as well; that build runs the cases only the emulation may run: device lengths that disagree
+with the host's (tests/kernel_emu/cases_emu_only.py).
+
 The emulation itself is pinned two ways: its cross-lane operations against their documented
 definitions (lane_ops_kat, which tests/test_lane_ops_gpu.py also runs on the MI355X), and the faults
 it must stop a launch for (emu_faults)."""
@@ -17,6 +21,9 @@ from conftest import ROOT, progress
 
 EMU = os.path.join(ROOT, "tests", "kernel_emu")
 BUILD = os.path.join(EMU, "build")
+
+
+ASAN_BUILD = os.path.join(EMU, "build-asan")
 
 
 @pytest.fixture(scope="module")
@@ -47,4 +54,14 @@ def test_gpu_tests_pass_on_the_emulated_kernels(emu_build):
     rc, out = _run([sys.executable, os.path.join(EMU, "run_gpu_tests.py"), "--build-dir", emu_build], 1800)
     tail = "\n".join(out.strip().splitlines()[-30:])
     progress(f"[emu] {tail.splitlines()[-1] if tail else ''}")
+    assert rc == 0, tail
+
+
+def test_lengths_the_host_did_not_check_under_address_sanitizer(emu_build):
+    """The kernels given device lengths that disagree with the host's (cases_emu_only.py), in the
+    AddressSanitizer build: every plain load and store is checked as well as every buffer access."""
+    if not all(os.path.exists(os.path.join(ASAN_BUILD, f)) for f in ("libkvb_hip.so", "libkvb_host.so")):
+        subprocess.run(["make", "-j", str(min(8, os.cpu_count() or 1)), "-C", EMU, "asan"], check=True)
+    rc, out = _run([sys.executable, os.path.join(EMU, "run_gpu_tests.py"), "--asan", "-k", "disagree"], 1800)
+    tail = "\n".join(out.strip().splitlines()[-30:])
     assert rc == 0, tail
