@@ -297,15 +297,25 @@ void record(hipEvent_t e);
 // ---- runtime API -----------------------------------------------------------------------------------------
 struct kvbemu_stream {
     unsigned flags = 0;
+    std::vector<std::function<hipError_t()>>* capture = nullptr;  // the graph being captured, if any
 };
 struct kvbemu_event {
     double t = 0.0;
 };
 struct kvbemu_graph {
-    int empty = 1;
+    std::vector<std::function<hipError_t()>> ops;  // captured work, in stream order
 };
 
 namespace kvbemu {
+hipError_t enqueue(hipStream_t s, std::function<hipError_t()> op) {
+    if (s && s->capture) {
+        s->capture->push_back(std::move(op));
+        return hipSuccess;
+    }
+    const hipError_t e = op();
+    if (e != hipSuccess && g_last_err == hipSuccess) g_last_err = e;
+    return e;
+}
 void record(hipEvent_t e) {
     e->t = std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
 }
@@ -376,12 +386,14 @@ hipError_t hipMemcpy(void* dst, const void* src, size_t bytes, hipMemcpyKind) {
     if (bytes) std::memmove(dst, src, bytes);
     return hipSuccess;
 }
-hipError_t hipMemcpyAsync(void* dst, const void* src, size_t bytes, hipMemcpyKind k, hipStream_t) {
-    return hipMemcpy(dst, src, bytes, k);
+hipError_t hipMemcpyAsync(void* dst, const void* src, size_t bytes, hipMemcpyKind k, hipStream_t s) {
+    return kvbemu::enqueue(s, [=]() { return hipMemcpy(dst, src, bytes, k); });
 }
-hipError_t hipMemsetAsync(void* dst, int value, size_t bytes, hipStream_t) {
-    if (bytes) std::memset(dst, value, bytes);
-    return hipSuccess;
+hipError_t hipMemsetAsync(void* dst, int value, size_t bytes, hipStream_t s) {
+    return kvbemu::enqueue(s, [=]() {
+        if (bytes) std::memset(dst, value, bytes);
+        return hipSuccess;
+    });
 }
 hipError_t hipMemcpyFromSymbol(void* dst, const void* sym, size_t bytes, size_t offset, hipMemcpyKind) {
     std::memcpy(dst, static_cast<const char*>(sym) + offset, bytes);
@@ -412,21 +424,31 @@ hipError_t hipEventDestroy(hipEvent_t e) {
     delete e;
     return hipSuccess;
 }
-hipError_t hipEventRecord(hipEvent_t e, hipStream_t) {
-    kvbemu::record(e);
-    return hipSuccess;
+hipError_t hipEventRecord(hipEvent_t e, hipStream_t s) {
+    return kvbemu::enqueue(s, [=]() {
+        kvbemu::record(e);
+        return hipSuccess;
+    });
 }
 hipError_t hipEventSynchronize(hipEvent_t) { return hipSuccess; }
 hipError_t hipEventElapsedTime(float* ms, hipEvent_t a, hipEvent_t b) {
     *ms = (float)((b->t - a->t) * 1e3);
     return hipSuccess;
 }
-// Graph capture is not emulated; an empty graph (which the runtime instantiates for a zero-step
-// capture) is.
-hipError_t hipStreamBeginCapture(hipStream_t, hipStreamCaptureMode) { return hipErrorNotSupported; }
-hipError_t hipStreamEndCapture(hipStream_t, hipGraph_t* g) {
+// Graphs: a capture records the stream's launches, fills, copies and event records as they are
+// issued; a launch of the instantiated graph runs them in that order.
+hipError_t hipStreamBeginCapture(hipStream_t s, hipStreamCaptureMode) {
+    if (!s || s->capture) return hipErrorInvalidValue;
+    s->capture = new std::vector<std::function<hipError_t()>>;
+    return hipSuccess;
+}
+hipError_t hipStreamEndCapture(hipStream_t s, hipGraph_t* g) {
     *g = nullptr;
-    return hipErrorNotSupported;
+    if (!s || !s->capture) return hipErrorInvalidValue;
+    *g = new kvbemu_graph{std::move(*s->capture)};
+    delete s->capture;
+    s->capture = nullptr;
+    return hipSuccess;
 }
 hipError_t hipGraphCreate(hipGraph_t* g, unsigned) {
     *g = new kvbemu_graph{};
@@ -434,10 +456,18 @@ hipError_t hipGraphCreate(hipGraph_t* g, unsigned) {
 }
 hipError_t hipGraphInstantiate(hipGraphExec_t* e, hipGraph_t g, hipGraphNode_t*, char*, size_t) {
     if (!g) return hipErrorInvalidValue;
-    *e = new kvbemu_graph{};
+    *e = new kvbemu_graph{g->ops};
     return hipSuccess;
 }
-hipError_t hipGraphLaunch(hipGraphExec_t e, hipStream_t) { return e ? hipSuccess : hipErrorInvalidValue; }
+hipError_t hipGraphLaunch(hipGraphExec_t e, hipStream_t s) {
+    if (!e) return hipErrorInvalidValue;
+    const kvbemu_graph* graph = e;
+    return kvbemu::enqueue(s, [graph]() {
+        for (const auto& op : graph->ops)
+            if (const hipError_t err = op(); err != hipSuccess) return err;
+        return hipSuccess;
+    });
+}
 hipError_t hipGraphDestroy(hipGraph_t g) {
     delete g;
     return hipSuccess;

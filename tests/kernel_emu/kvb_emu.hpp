@@ -604,21 +604,29 @@ namespace kvbemu {
 // Runs grid x block threads of `body` (the kernel call with its arguments), workgroup by workgroup.
 hipError_t launch(dim3 grid, dim3 block, const std::function<void()>& body);
 void record(hipEvent_t e);
+// Stream capture: while `s` captures, its work is appended to the graph being captured instead of
+// running (`op` returns what the work would have returned); otherwise op runs now.
+hipError_t enqueue(hipStream_t s, std::function<hipError_t()> op);
 }  // namespace kvbemu
 
 template <typename... KArgs, typename... Args>
-void hipLaunchKernelGGL(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t /*lds*/, hipStream_t /*s*/,
+void hipLaunchKernelGGL(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t /*lds*/, hipStream_t s,
                         Args... args) {
-    const std::function<void()> body = [&]() { kernel(args...); };
-    (void)::kvbemu::launch(grid, block, body);
+    (void)::kvbemu::enqueue(s, [=]() {  // (the arguments by value: a captured launch runs later)
+        const std::function<void()> body = [&]() { kernel(args...); };
+        return ::kvbemu::launch(grid, block, body);
+    });
 }
 template <typename... KArgs, typename... Args>
-void hipExtLaunchKernelGGL(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t /*lds*/, hipStream_t /*s*/,
+void hipExtLaunchKernelGGL(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t /*lds*/, hipStream_t s,
                            hipEvent_t start, hipEvent_t stop, unsigned /*flags*/, Args... args) {
-    if (start) ::kvbemu::record(start);
-    const std::function<void()> body = [&]() { kernel(args...); };
-    (void)::kvbemu::launch(grid, block, body);
-    if (stop) ::kvbemu::record(stop);
+    (void)::kvbemu::enqueue(s, [=]() {
+        if (start) ::kvbemu::record(start);
+        const std::function<void()> body = [&]() { kernel(args...); };
+        const hipError_t e = ::kvbemu::launch(grid, block, body);
+        if (stop) ::kvbemu::record(stop);
+        return e;
+    });
 }
 
 extern "C" const char* kvbemu_last_error(void);

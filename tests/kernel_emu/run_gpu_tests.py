@@ -6,8 +6,9 @@ libkvb_hip.so with the same C ABI. With KVB_BUILD_DIR pointing at that build the
 and the GPU tests run as they are: the same cases, the same oracle, the same tolerances and
 bit-identity checks, on the kernels' own source code. Left out are the tests that measure the
 hardware or need the HIP runtime itself: full-size configurations (hours on the emulation), the
-4 GiB read probe, graph capture, stream switching through libamdhip64, and the C++ programs and
-benchmarks that load the GPU build.
+4 GiB read probe, stream switching through libamdhip64, and the C++ programs and benchmarks that
+load the GPU build. Graph capture is emulated: a captured stream records its work, and a launch of
+the graph replays it in order.
 
 With --asan the libraries are the AddressSanitizer build (make -C tests/kernel_emu asan), so every
 plain load and store the kernels make is checked against its allocation, in addition to the
@@ -32,7 +33,7 @@ ASAN_BUILD = os.path.join(HERE, "build-asan")
 CXX = "/opt/rocm/lib/llvm/bin/clang++"
 
 FILES = ["tests/test_gpu_parity.py", "tests/test_gpu_groups.py", "tests/test_gpu_pair.py",
-         "tests/test_gpu_writer.py", "tests/test_zz_no_alloc.py",
+         "tests/test_gpu_writer.py", "tests/test_gpu_graph.py", "tests/test_zz_no_alloc.py",
          "tests/kernel_emu/cases_emu_only.py"]  # (the last: lengths the host did not check)
 # hardware measurements, or calls into the HIP runtime itself
 HARDWARE = "not full_size and not stream_switch and not read_bandwidth"
@@ -42,6 +43,7 @@ SLOW = [
     "tests/test_gpu_parity.py::test_random_layouts[11]",
     "tests/test_gpu_parity.py::test_random_layouts[23]",
     "tests/test_gpu_parity.py::test_fused_merge_reads_fresh_partitions",
+    "tests/test_gpu_graph.py::test_graph_replays_match_eager",
 ]
 
 
