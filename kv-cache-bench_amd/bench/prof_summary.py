@@ -99,7 +99,8 @@ def main(cfg, out):
           f"{timed[0][1]['Accum_VGPR_Count']} AGPR, LDS {timed[0][1]['LDS_Block_Size']} B).\n")
     print("## Commands (from the repository root on the GPU box)\n")
     print("```")
-    print(f"bash kv-cache-bench_amd/bench/profile.sh {cfg} gpurun_out/prof_{cfg}")
+    root = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    print(f"bash kv-cache-bench_amd/bench/profile.sh {cfg} {os.path.relpath(out, root)}")
     print("```\n")
     print("That script runs, from /tmp with TMPDIR=/tmp (R = the repository root):\n")
     print("```")
