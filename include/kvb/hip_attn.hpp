@@ -76,9 +76,11 @@ inline int auto_part_tokens(const Shape& s, int max_len) {
 int mi355x_part_tokens(const Shape& s, int max_len, int min_groups = 256, int min_part = 256, int max_part = 4096);
 // The policy for a batch given its lengths. Lengths that are not all equal make a ragged batch,
 // which runs in the longest-first work order. There, shorter partitions give the schedule finer
-// pieces at its end, so max_part is capped at kRaggedMaxPart. Measured on MI355X (c5): 330 us at
-// 2048 against 340 us at 4096 (fp16), 182 against 183 (int8).
-constexpr int kRaggedMaxPart = 2048;
+// pieces at its end, so the partition is capped at kRaggedMaxPart (not a power of two: 7 x 512).
+// Measured on MI355X (c5, medians of 30, three sweeps on two boxes): fp16 328.6-332.3 us at 3584
+// against 333.9-335.8 at 2048, 330.5-331.3 at 2560, 332.2-333.1 at 3072, 330.2-331.2 at 3840 and
+// 341.0-341.5 at 4096; int8 182.1-183.1 against 183.6-184.5 at 2048 and 185.5-186.7 at 4096.
+constexpr int kRaggedMaxPart = 3584;
 int mi355x_part_tokens(const Shape& s, std::span<const int> lens, int min_groups = 256, int min_part = 256,
                        int max_part = 4096);
 // min_groups of the policy: 256 (one workgroup per CU), or 512 (two) when a K or V row is under

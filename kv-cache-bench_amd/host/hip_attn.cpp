@@ -135,8 +135,8 @@ int mi355x_part_tokens(const Shape& s, std::span<const int> lens, int min_groups
         max_len = std::max(max_len, len);
         ragged = ragged || len != lens[0];
     }
-    if (ragged) max_part = std::max(min_part, std::min(max_part, kRaggedMaxPart));
-    return mi355x_part_tokens(s, max_len, min_groups, min_part, max_part);
+    const int part = mi355x_part_tokens(s, max_len, min_groups, min_part, max_part);
+    return ragged ? std::max(std::min(min_part, part), std::min(part, kRaggedMaxPart)) : part;
 }
 
 kvb_paged_args c_args(const PagedArgs& a) {
