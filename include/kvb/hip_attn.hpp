@@ -80,6 +80,10 @@ int mi355x_part_tokens(const Shape& s, int max_len, int min_groups = 256, int mi
 // Measured on MI355X (c5, medians of 30, three sweeps on two boxes): fp16 328.6-332.3 us at 3584
 // against 333.9-335.8 at 2048, 330.5-331.3 at 2560, 332.2-333.1 at 3072, 330.2-331.2 at 3840 and
 // 341.0-341.5 at 4096; int8 182.1-183.1 against 183.6-184.5 at 2048 and 185.5-186.7 at 4096.
+// c5's pages hold 64 tokens, so a partition spans at most 56 blocks, whose ids (and int8 scales)
+// the kernel keeps in lanes (up to 64). With pages under 56 tokens a 3584-token partition spans
+// more, and each tile reads its block id instead; such a batch was not measured here, and a caller
+// may pass max_part = 64 * page_size to keep the ids in lanes.
 constexpr int kRaggedMaxPart = 3584;
 int mi355x_part_tokens(const Shape& s, std::span<const int> lens, int min_groups = 256, int min_part = 256,
                        int max_part = 4096);
