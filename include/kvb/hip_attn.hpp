@@ -75,16 +75,27 @@ inline int auto_part_tokens(const Shape& s, int max_len) {
 // one workgroup per CU (min_groups 256, the default).
 int mi355x_part_tokens(const Shape& s, int max_len, int min_groups = 256, int min_part = 256, int max_part = 4096);
 // The policy for a batch given its lengths. Lengths that are not all equal make a ragged batch,
-// which runs in the longest-first work order. There, shorter partitions give the schedule finer
-// pieces at its end, so the partition is capped at kRaggedMaxPart (not a power of two: 7 x 512).
-// Measured on MI355X (c5, medians of 30, three sweeps on two boxes): fp16 328.6-332.3 us at 3584
-// against 333.9-335.8 at 2048, 330.5-331.3 at 2560, 332.2-333.1 at 3072, 330.2-331.2 at 3840 and
-// 341.0-341.5 at 4096; int8 182.1-183.1 against 183.6-184.5 at 2048 and 185.5-186.7 at 4096.
-// c5's pages hold 64 tokens, so a partition spans at most 56 blocks, whose ids (and int8 scales)
-// the kernel keeps in lanes (up to 64). With pages under 56 tokens a 3584-token partition spans
-// more, and each tile reads its block id instead; such a batch was not measured here, and a caller
-// may pass max_part = 64 * page_size to keep the ids in lanes.
-constexpr int kRaggedMaxPart = 3584;
+// which runs in the longest-first work order. Its partition trades the schedule's end (finer pieces
+// with shorter partitions) against each workgroup's fixed cost (prologue, epilogue, merge), paid
+// once per partition. The partition is capped at ragged_part_cap(max_len): 2048 while the longest
+// sequence is under two 3584-token partitions, 4096 once it spans eight 4096-token ones, 3584 (7 x
+// 512) between. Measured on MI355X, 32 q / 8 KV heads, head_dim 128, page 64, cold steps, us at
+// partitions 2048 / 3584 / 4096 (the cap's choice marked *):
+//   64 lengths ~U[1, 4096]:   fp16 95.8* / 100.6 / 109.7; int8 58.2* / 60.3 / 62.8
+//   64 lengths ~U[1, 8192]:   fp16 175.7 / 176.0* / 182.3; int8 99.6 / 99.6* / 102.6
+//   128 lengths ~U[1, 8192]:  fp16 337.8 / 333.2* / 329.4; int8 190.3 / 183.4* / 180.1
+//   32 lengths ~U[1, 16384]:  fp16 182.4-182.7 / 181.8-183.5* / 186.7; int8 103.3-104.4 / 102.0-102.4* / 104.0
+//   c5, 72 lengths ~U[1, 16384]: fp16 333.9-335.8 / 328.6-332.3* / 341.0-341.5;
+//       int8 183.6-184.5 / 182.1-183.1* / 185.5-186.7
+//   64 lengths ~U[1, 32768]:  fp16 688.9 / 676.5 / 671.9*; int8 375.8 / 363.8 / 360.0*
+//   16 lengths ~U[1, 65536]:  fp16 399.6 / 404.0 / 389.9*; int8 222.3 / 220.3 / 213.4*
+// Sizes in between were not better: c5 at 2560-3328 and 3840 ran 0-1.5% slower than at 3584, and
+// 32 lengths ~U[1, 16384] ran 2.5-3% slower at 2560 (fp16) than at 2048 or 3584.
+// With pages under 64 tokens a partition over 4096 / 64 pages spans more than 64 blocks, whose ids
+// the kernel then reads per tile instead of keeping them in lanes; a caller with such pages may
+// pass max_part = 64 * page_size.
+constexpr int kRaggedShortCap = 2048, kRaggedCap = 3584, kRaggedLongCap = 4096;
+int ragged_part_cap(int max_len);
 int mi355x_part_tokens(const Shape& s, std::span<const int> lens, int min_groups = 256, int min_part = 256,
                        int max_part = 4096);
 // min_groups of the policy: 256 (one workgroup per CU), or 512 (two) when a K or V row is under

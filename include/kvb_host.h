@@ -53,7 +53,8 @@ int kvbh_poison_paged(int batch, int num_kv_heads, int head_dim, int page_size, 
 /* The MI355X partition policy (kvb::mi355x_part_tokens). */
 int kvbh_mi355x_part_tokens(int batch, int num_heads, int num_kv_heads, int head_dim, int max_len, int min_groups,
                             int min_part, int max_part);
-/* The same policy given the batch's lengths (lens[batch]): a ragged batch caps the partition at 3584. */
+/* The same policy given the batch's lengths (lens[batch]): a ragged batch caps the partition at
+ * kvb::ragged_part_cap: 2048, 3584 or 4096 by its longest sequence (3584 for c5). */
 int kvbh_mi355x_part_tokens_lens(int batch, int num_heads, int num_kv_heads, int head_dim, const int* lens,
                                  int min_groups, int min_part, int max_part);
 

@@ -185,7 +185,8 @@ def mi355x_part_tokens(shape, max_len, min_groups=256, min_part=256, max_part=40
 
 def mi355x_part_tokens_for(shape, lens, min_groups=256, min_part=256, max_part=4096) -> int:
     """The MI355X partition policy given the batch's lengths (kvb::mi355x_part_tokens(shape, lens)):
-    a ragged batch caps the partition at 3584 (kvb::kRaggedMaxPart)."""
+    a ragged batch caps the partition at kvb::ragged_part_cap(max_len): 2048 while the longest sequence
+    is under 2 x 3584 tokens, 4096 from 8 x 4096, 3584 between."""
     lens = np.ascontiguousarray(lens, np.int32)
     return host.kvbh_mi355x_part_tokens_lens(shape.batch, shape.num_heads, shape.num_kv_heads, shape.head_dim,
                                              _ptr(lens), min_groups, min_part, max_part)

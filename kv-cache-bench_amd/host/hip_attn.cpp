@@ -136,7 +136,12 @@ int mi355x_part_tokens(const Shape& s, std::span<const int> lens, int min_groups
         ragged = ragged || len != lens[0];
     }
     const int part = mi355x_part_tokens(s, max_len, min_groups, min_part, max_part);
-    return ragged ? std::max(std::min(min_part, part), std::min(part, kRaggedMaxPart)) : part;
+    return ragged ? std::max(std::min(min_part, part), std::min(part, ragged_part_cap(max_len))) : part;
+}
+
+int ragged_part_cap(int max_len) {
+    if (max_len >= 8 * kRaggedLongCap) return kRaggedLongCap;
+    return max_len >= 2 * kRaggedCap ? kRaggedCap : kRaggedShortCap;
 }
 
 kvb_paged_args c_args(const PagedArgs& a) {

@@ -84,12 +84,17 @@ def test_mi355x_partition_policy(kvb):
     # c3 (B 16, 32/8 heads, 8k): 16 * 8 workgroups per partition
     assert kvb.mi355x_part_tokens(kvb.Shape(16, 32, 8, 128), 8192) == 4096
     assert kvb.mi355x_part_tokens(kvb.Shape(16, 32, 8, 128), 8192, min_groups=512) == 2048
-    # a ragged batch (lengths not all equal) caps the partition at 3584 (7 x 512): c5's lengths ->
-    # 3584, c4's equal lengths keep 4096; a ragged choice already under the cap stays; the cap
-    # yields to a larger min_part; an all-empty batch gets the floor
+    # a ragged batch (lengths not all equal) caps the partition at 2048 while its longest sequence is
+    # under 2 x 3584 tokens, 4096 from 8 x 4096, 3584 between: c5's lengths -> 3584; c4's equal
+    # lengths keep 4096; the cap yields to a larger min_part; an all-empty batch gets the floor
     c5 = kvb.Shape(72, 32, 8, 128)
+    assert max(kvb.c5_lengths()) >= 2 * 3584
     assert kvb.mi355x_part_tokens_for(c5, kvb.c5_lengths()) == 3584
     assert kvb.mi355x_part_tokens_for(c5, kvb.c5_lengths(), min_part=4096) == 4096
+    s64 = kvb.Shape(64, 32, 8, 128)
+    for longest, cap in ((4096, 2048), (7167, 2048), (7168, 3584), (32767, 3584), (32768, 4096), (65536, 4096)):
+        lens = [100] * 63 + [longest]
+        assert kvb.mi355x_part_tokens_for(s64, lens) == cap, (longest, cap)
     assert kvb.mi355x_part_tokens_for(kvb.Shape(4, 64, 8, 128), [32768] * 4) == 4096
     assert kvb.mi355x_part_tokens_for(kvb.Shape(2, 64, 8, 128), [32768, 100]) == 2048
     assert kvb.mi355x_part_tokens_for(kvb.Shape(3, 8, 2, 64), [0, 0, 0]) == 256
