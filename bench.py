@@ -25,7 +25,8 @@ sys.path.insert(0, ROOT)
 import __graft_entry__ as graft  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_c4_decode.json")
+sys.path.insert(0, os.path.join(ROOT, "kv-cache-bench_amd", "bench"))
+import build_info  # noqa: E402  (the environment record)
 
 
 def log(msg):
@@ -103,24 +104,29 @@ def empty_steps(kvb, w, part, steps=30):
 
 
 def cpu_threads():
-    """Threads for the CPU baseline: the CPUs this process may run on (the counterpart of the
-    reference's std::thread::hardware_concurrency, bench/bench.cpp:94), at most 16, the CPU share of
-    one GPU on the machines this runs on."""
-    try:
-        n = len(os.sched_getaffinity(0))
-    except (AttributeError, OSError):
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+    """Threads for the CPU baseline: every CPU this process may run on, the counterpart of the
+    reference's std::thread::hardware_concurrency (bench/bench.cpp:94)."""
+    return max(1, build_info.cpu_threads())
 
 
 def cpu_model():
     """The host CPU's model name (/proc/cpuinfo), and the core count the OS reports."""
-    try:
-        with open("/proc/cpuinfo") as f:
-            name = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "unknown")
-    except OSError:
-        name = "unknown"
-    return f"{name}, {os.cpu_count()} logical CPUs"
+    return f"{build_info.cpu_model()}, {os.cpu_count()} logical CPUs"
+
+
+def traffic_record(config, kernel):
+    """profiles/traffic_<config>.json, the per-launch HBM traffic and L2 hit rate that rocprofv3
+    counters gave for this configuration (prof_summary.py), and None in its place (with the reason)
+    unless it was measured on the kernel this run launches: a record whose kernel name differs
+    describes other code."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{config}.json")
+    if not os.path.exists(path):
+        return None, f"no {os.path.relpath(path, ROOT)}"
+    with open(path) as f:
+        rec = json.load(f)
+    if rec.get("kernel_name") != kernel:
+        return None, f"{os.path.relpath(path, ROOT)} was measured on {rec.get('kernel_name')!r}, this run launches {kernel!r}"
+    return rec, None
 
 
 def cpu_baseline(kvb, oracle, w, c, seconds_budget=20.0, max_bytes=1 << 30):
@@ -208,10 +214,12 @@ def main():
               "on its own shard of sequences / KV heads); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    loadavg = os.getloadavg()  # before this run adds its own load
     kvb = graft.load_package()
     if not kvb.gpu_available():
         print("bench.py: no GPU", file=sys.stderr)
         sys.exit(1)
+    env = build_info.env_record(kvb, loadavg)
     log(f"device: {kvb.device_name()}")
     kvb.set_pair_mode(args.pair)
     # The probe runs first, and nothing is freed until every GPU measurement is done: on these boxes
@@ -226,7 +234,7 @@ def main():
         probe_gbps = round((4 << 30) / (statistics.median(pt) * 1e-3) / 1e9, 1)
         keep.append(probe)
     t_setup = time.perf_counter()
-    w, c, cfg = kvb.make_config(args.config, threads=16)
+    w, c, cfg = kvb.make_config(args.config, threads=cpu_threads())
     part = kvb.config_part(cfg, w) if args.part is None else args.part
     dev = kvb.DeviceCase(w, c)
     devi = None
@@ -234,7 +242,7 @@ def main():
         # c4's shape with an int8 cache (per-(page, KV head) scales), for the int8 / fp16 speed ratio.
         # Its pools are allocated here, with the fp16 ones, as a server allocates its KV pools at start:
         # allocated after the other measurements they have landed where int8 ran up to 9% slower.
-        wi = kvb.Workload(w.shape, "i8", list(w.lens), seed=32768, q_amp=1.0, dist="normal", threads=16)
+        wi = kvb.Workload(w.shape, "i8", list(w.lens), seed=32768, q_amp=1.0, dist="normal", threads=cpu_threads())
         ci = kvb.PagedCache(wi, 128, 32768 * 131 + 128, pool_factor=1.25, poison=False)
         devi = kvb.DeviceCase(wi, ci)
     nparts = dev.max_parts(part)
@@ -251,11 +259,12 @@ def main():
     log(f"{args.config}: step median {med * 1e3:.1f} us (mean {kernel_avg * 1e3:.1f} us), {value:.0f} GB/s; "
         f"wall {wall:.3f}s for {args.steps} steps")
 
-    traffic = tcc_hit = None
-    if args.config == "c4" and os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            rec = json.load(f)
-        traffic, tcc_hit = rec.get("bytes_per_launch"), rec.get("tcc_hit_rate")
+    kernel = dev.kernel_name(part)
+    rec, why = traffic_record(args.config, kernel)
+    traffic = rec["bytes_per_launch"] if rec else None
+    tcc_hit = rec["tcc_hit_rate"] if rec else None
+    if why:
+        log(f"roofline.traffic: null ({why})")
 
     extras = {}
     if w.kv_type == kvb.KV_I8:
@@ -324,9 +333,11 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "tcc_hit_rate": tcc_hit,
-                     "kernel": "paged_decode", "kernel_avg_us": round(kernel_avg * 1e3, 2),
+                     "traffic_source": f"profiles/traffic_{args.config}.json" if rec else why,
+                     "kernel": kernel, "kernel_avg_us": round(kernel_avg * 1e3, 2),
                      "bytes_per_launch": bytes_step},
         "cpu_baseline": cpu,
+        "env": env,
     }
     line.update(extras)
     print(json.dumps(line), flush=True)

@@ -78,8 +78,8 @@ int mi355x_part_tokens(const Shape& s, int max_len, int min_groups = 256, int mi
 // which runs in the longest-first work order. Its partition trades the schedule's end (finer pieces
 // with shorter partitions) against each workgroup's fixed cost (prologue, epilogue, merge), paid
 // once per partition. The partition is capped at ragged_part_cap(max_len): 2048 while the longest
-// sequence is under two 3584-token partitions, 4096 once it spans eight 4096-token ones, 3584 (7 x
-// 512) between. Measured on MI355X, 32 q / 8 KV heads, head_dim 128, page 64, cold steps, us at
+// sequence is under two 3584-token partitions, 4096 once it spans seven 4096-token ones (28672
+// tokens: uniform draws up to 32768 rarely reach 32768 itself), 3584 (7 x 512) between. Measured on MI355X, 32 q / 8 KV heads, head_dim 128, page 64, cold steps, us at
 // partitions 2048 / 3584 / 4096 (the cap's choice marked *):
 //   64 lengths ~U[1, 4096]:   fp16 95.8* / 100.6 / 109.7; int8 58.2* / 60.3 / 62.8
 //   64 lengths ~U[1, 8192]:   fp16 175.7 / 176.0* / 182.3; int8 99.6 / 99.6* / 102.6

@@ -34,6 +34,25 @@ enum { KVB_KV_F32 = 0, KVB_KV_F16 = 1, KVB_KV_I8 = 2 };
 int kvb_gpu_available(void);
 /* Device name into buf (device_name, src/metal_attn.hpp:14). */
 int kvb_device_name(char* buf, size_t cap);
+/* What the environment record of a result holds about the device and the HIP stack (the counterpart
+ * of the reference's scripts/env.sh, which records machine, toolchain and load beside its results). */
+typedef struct kvb_device_info_t {
+    int runtime_version;  /* hipRuntimeGetVersion */
+    int driver_version;   /* hipDriverGetVersion */
+    int device;           /* the library's device ordinal */
+    int compute_units;
+    int clock_khz;        /* peak shader clock (hipDeviceAttributeClockRate) */
+    int memory_clock_khz; /* hipDeviceAttributeMemoryClockRate */
+    int memory_bus_bits;
+    int l2_bytes;         /* one XCD's L2 as the runtime reports it */
+    size_t total_memory;
+    size_t free_memory;   /* at the call */
+    char name[256];
+    char arch[64];        /* gcnArchName, e.g. gfx950:sramecc+:xnack- */
+    char pci_bus_id[32];
+} kvb_device_info_t;
+/* Fills *info for the library's device. No reference counterpart beyond device_name. */
+int kvb_device_info(kvb_device_info_t* info);
 /* Message of the last call that did not return KVB_OK ("" if none). */
 const char* kvb_last_error(void);
 /* Runs the library's work on `stream` (a hipStream_t; NULL = the library's own stream, created
@@ -149,9 +168,13 @@ int kvb_run_paged_steps(const kvb_paged_args* a, int steps, double* ms);
  * the capture, and freed by kvb_graph_destroy), so no later call can move them; it holds the
  * caller's pointers from `a` (q, k, v, tables, lengths, scales, out), which must stay valid and keep
  * their shapes while it exists. The captured steps are the same kernels, in the same order, as
- * kvb_run_paged_steps: the same bits. They allocate nothing and contain no memset node. Same
- * refusals as kvb_run_paged, plus KVB_EINVAL for steps < 1, a->workspace set, or pipelined mode.
- * *graph receives an opaque handle. */
+ * kvb_run_paged_steps: the same bits. They allocate nothing and contain no memset node. The grid
+ * and the work order are fixed at capture from host_seq_lens. Equal lengths at capture (the plain
+ * grid): each replay serves the device seq_lens as they are then, clamped to the captured max_len.
+ * Lengths not all equal (the longest-first order): every replay needs device seq_lens equal to the
+ * captured host_seq_lens; lengths that make a different number of work items turn the replay into a
+ * no-op that leaves out as it was and reports no error. Same refusals as kvb_run_paged, plus
+ * KVB_EINVAL for steps < 1, a->workspace set, or pipelined mode. *graph receives an opaque handle. */
 int kvb_graph_capture_paged(const kvb_paged_args* a, int steps, void** graph);
 /* Launches a captured graph on the library's current stream. *ms = GPU time of the launch (hipEvent
  * pair); 0 in pipelined mode. KVB_EINVAL for a null handle. */
@@ -169,6 +192,16 @@ int kvb_run_paged_split(const kvb_paged_args* a, double* decode_ms, double* redu
  * the decode's memory traffic alone, which bounds the decode kernel from below. Same refusals as
  * kvb_run_paged, plus KVB_EINVAL unless page_size and the partition are multiples of 16. */
 int kvb_run_paged_loads(const kvb_paged_args* a, double* ms);
+/* Measurement aid, not in the reference: one launch of a kernel that does nothing, `workgroups`
+ * workgroups of `threads` threads (a multiple of 64, at most 1024), timed like a decode step (events
+ * stamped by the dispatch): the floor that dispatch and completion put under any kernel of that grid.
+ * KVB_EINVAL for other sizes. */
+int kvb_run_empty_grid(int workgroups, int threads, double* ms);
+/* Not in the reference: the name of the paged_decode kernel that kvb_run_paged (loads_only 0) or
+ * kvb_run_paged_loads (1) launches for these arguments, as rocprofv3 prints it, followed by
+ * " + paged_reduce" where the step falls back to the two-kernel form; nothing is launched. A
+ * profile of a run is attached to a result only when the names agree. Same refusals as those calls. */
+int kvb_paged_kernel_name(const kvb_paged_args* a, int loads_only, char* buf, size_t cap);
 /* Tuning switch, not in the reference: when a decode workgroup computes two consecutive partitions
  * instead of one. KVB_PAIR_AUTO (the default): when the plain (sequence, partition) grid would put
  * two or more workgroups on every CU; KVB_PAIR_OFF: never; KVB_PAIR_ALWAYS: whenever it is allowed.

@@ -68,12 +68,22 @@ class CacheArgsC(ctypes.Structure):
                [(n, _p) for n in ("contig", "paged", "scales", "block_table", "seq_lens", "host_seq_lens")]
 
 
+class DeviceInfoC(ctypes.Structure):
+    """struct kvb_device_info_t (include/kvb_hip.h)."""
+
+    _fields_ = [(n, _i) for n in ("runtime_version", "driver_version", "device", "compute_units", "clock_khz",
+                                  "memory_clock_khz", "memory_bus_bits", "l2_bytes")] + \
+               [("total_memory", _sz), ("free_memory", _sz), ("name", ctypes.c_char * 256),
+                ("arch", ctypes.c_char * 64), ("pci_bus_id", ctypes.c_char * 32)]
+
+
 _PA = ctypes.POINTER(PagedArgsC)
 _NA = ctypes.POINTER(NaiveArgsC)
 _CA = ctypes.POINTER(CacheArgsC)
 _SIGS = {
     "kvb_gpu_available": ([], _i),
     "kvb_device_name": ([ctypes.c_char_p, _sz], _i),
+    "kvb_device_info": ([ctypes.POINTER(DeviceInfoC)], _i),
     "kvb_last_error": ([], ctypes.c_char_p),
     "kvb_set_stream": ([_p], _i),
     "kvb_synchronize": ([], _i),
@@ -94,6 +104,8 @@ _SIGS = {
     "kvb_graph_destroy": ([ctypes.c_void_p], _i),
     "kvb_run_paged_split": ([_PA, _d, _d], _i),
     "kvb_run_paged_loads": ([_PA, _d], _i),
+    "kvb_run_empty_grid": ([_i, _i, _d], _i),
+    "kvb_paged_kernel_name": ([_PA, _i, ctypes.c_char_p, _sz], _i),
     "kvb_set_pair_mode": ([_i], _i),
     "kvb_run_paged_noalloc": ([_PA], _i),
     "kvb_run_naive": ([_NA, _d], _i),
@@ -164,6 +176,24 @@ def device_name() -> str:
     return buf.value.decode()
 
 
+def device_info() -> dict:
+    """The device and HIP stack (kvb_device_info): runtime and driver versions, name, architecture,
+    PCI bus id, compute units, clocks, memory."""
+    d = DeviceInfoC()
+    check(hip.kvb_device_info(ctypes.byref(d)), "device_info")
+    out = {n: getattr(d, n) for n, _ in DeviceInfoC._fields_}
+    for n in ("name", "arch", "pci_bus_id"):
+        out[n] = out[n].decode(errors="replace")
+    return out
+
+
+def run_empty_grid(workgroups, threads=256) -> float:
+    """GPU ms of one launch of a kernel that does nothing (kvb_run_empty_grid): the dispatch floor."""
+    ms = ctypes.c_double()
+    check(hip.kvb_run_empty_grid(workgroups, threads, ctypes.byref(ms)), "run_empty_grid")
+    return ms.value
+
+
 def auto_part_tokens(batch, num_kv_heads, max_len) -> int:
     """src/metal_attn.hpp:43-51, through the C ABI."""
     return hip.kvb_auto_part_tokens(batch, num_kv_heads, max_len)
@@ -186,7 +216,7 @@ def mi355x_part_tokens(shape, max_len, min_groups=256, min_part=256, max_part=40
 def mi355x_part_tokens_for(shape, lens, min_groups=256, min_part=256, max_part=4096) -> int:
     """The MI355X partition policy given the batch's lengths (kvb::mi355x_part_tokens(shape, lens)):
     a ragged batch caps the partition at kvb::ragged_part_cap(max_len): 2048 while the longest sequence
-    is under 2 x 3584 tokens, 4096 from 8 x 4096, 3584 between."""
+    is under 2 x 3584 tokens, 4096 from 7 x 4096, 3584 between."""
     lens = np.ascontiguousarray(lens, np.int32)
     return host.kvbh_mi355x_part_tokens_lens(shape.batch, shape.num_heads, shape.num_kv_heads, shape.head_dim,
                                              _ptr(lens), min_groups, min_part, max_part)
@@ -436,6 +466,14 @@ class DeviceCase:
         a = self.args(part_tokens)
         check(hip.kvb_run_paged_loads(ctypes.byref(a), ctypes.byref(ms)), "run_paged_loads")
         return ms.value
+
+    def kernel_name(self, part_tokens=0, loads_only=False) -> str:
+        """The paged_decode kernel run() (or run_loads()) launches here, as rocprofv3 names it
+        (kvb_paged_kernel_name); launches nothing."""
+        buf = ctypes.create_string_buffer(512)
+        a = self.args(part_tokens)
+        check(hip.kvb_paged_kernel_name(ctypes.byref(a), int(loads_only), buf, 512), "paged_kernel_name")
+        return buf.value.decode()
 
     def output(self):
         s = self.w.shape

@@ -17,6 +17,7 @@
 // attention_reference, from the reference's kvref built as a shared library and named by
 // --cpu-ref=LIB; this program does not link it, and without --cpu-ref there are no such rows.
 #include <dlfcn.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <chrono>
@@ -32,6 +33,7 @@
 #include <vector>
 
 #include "kvb/workload.hpp"
+#include "kvb_hip.h"
 
 namespace {
 
@@ -578,9 +580,74 @@ int mode_sweep(const Options& o, const GpuTimer& timer, const CpuReference& cpu_
     return 0;
 }
 
+// ---- environment record --------------------------------------------------------------------
+// The "# env" header line: the build (build_info.json beside this program, written by the package
+// Makefile: commit, dirty flag), the HIP runtime and driver, the ROCm release, the device, the CPU
+// and the load average before the run (the reference's scripts/env.sh records the same beside its
+// results).
+
+std::string read_file(const std::string& path) {
+    std::string out;
+    if (FILE* f = std::fopen(path.c_str(), "r")) {
+        char buf[4096];
+        size_t n;
+        while ((n = std::fread(buf, 1, sizeof buf, f)) > 0) out.append(buf, n);
+        std::fclose(f);
+    }
+    return out;
+}
+
+// The value of "key" in a flat JSON object as text: a string's contents, or the literal.
+std::string json_field(const std::string& text, const std::string& key) {
+    const size_t k = text.find("\"" + key + "\"");
+    if (k == std::string::npos) return "unknown";
+    size_t i = text.find(':', k);
+    if (i == std::string::npos) return "unknown";
+    i = text.find_first_not_of(" \t\n", i + 1);
+    if (i == std::string::npos) return "unknown";
+    if (text[i] == '"') {
+        const size_t e = text.find('"', i + 1);
+        return e == std::string::npos ? "unknown" : text.substr(i + 1, e - i - 1);
+    }
+    const size_t e = text.find_first_of(",}\n", i);
+    return text.substr(i, e == std::string::npos ? std::string::npos : e - i);
+}
+
+std::string trim(std::string s) {
+    while (!s.empty() && (s.back() == '\n' || s.back() == ' ')) s.pop_back();
+    return s;
+}
+
+void print_env(const std::string& loadavg, int threads) {
+    char exe[4096] = {0};
+    const ssize_t n = readlink("/proc/self/exe", exe, sizeof exe - 1);
+    std::string dir = n > 0 ? std::string(exe, size_t(n)) : std::string();
+    dir = dir.substr(0, dir.find_last_of('/') + 1);
+    const std::string built = read_file(dir + "build_info.json");
+    std::string cpu = "unknown";
+    const std::string info = read_file("/proc/cpuinfo");
+    if (const size_t m = info.find("model name"); m != std::string::npos) {
+        const size_t c = info.find(':', m), e = info.find('\n', m);
+        if (c != std::string::npos && c < e) cpu = info.substr(c + 2, e - c - 2);
+    }
+    kvb_device_info_t d{};
+    const bool dev = kvb_device_info(&d) == KVB_OK;
+    std::printf("# env commit=%s dirty=%s built_at=%s hipcc=%s hip_runtime=%d hip_driver=%d rocm=%s device=\"%s\" "
+                "arch=%s pci=%s cus=%d sclk_mhz=%d mclk_mhz=%d hbm_gib=%.1f cpu=\"%s\" cpu_threads=%d loadavg=%s\n",
+                json_field(built, "commit").c_str(), json_field(built, "dirty").c_str(),
+                json_field(built, "built_at").c_str(), json_field(built, "hipcc").c_str(), dev ? d.runtime_version : 0,
+                dev ? d.driver_version : 0, trim(read_file("/opt/rocm/.info/version")).c_str(), d.name, d.arch,
+                d.pci_bus_id, d.compute_units, d.clock_khz / 1000, d.memory_clock_khz / 1000,
+                double(d.total_memory) / double(1ull << 30), cpu.c_str(), threads, loadavg.c_str());
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
+    std::string loadavg = trim(read_file("/proc/loadavg"));  // before this run adds its own load
+    loadavg = loadavg.substr(0, loadavg.find(' ', loadavg.find(' ', loadavg.find(' ') + 1) + 1));
+    for (char& ch : loadavg)
+        if (ch == ' ') ch = ',';
     Options o;
     if (!parse(argc, argv, o) || !apply_config(o)) return 2;
     if (o.parts.empty() || o.reps < 1 || o.warmup < 0 || o.cpu_reps < 1) {
@@ -602,6 +669,7 @@ int main(int argc, char** argv) {
                 device_name().c_str(), o.shape.batch, o.shape.num_heads, o.shape.num_kv_heads, o.shape.head_dim,
                 o.reps, o.warmup, o.cpu_reps, threads, o.flush, kSimdGroups, o.sync ? "sync" : "pipelined",
                 o.dist == Dist::normal ? "normal" : "uniform", o.pool);
+    print_env(loadavg, threads);
     const GpuTimer timer(o);
     if (o.bw) return mode_bw(o, timer);
     if (!o.dump.empty()) return mode_dump(o);

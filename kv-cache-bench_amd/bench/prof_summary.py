@@ -1,6 +1,8 @@
 """Summarise the measurements of profile.sh CONFIG OUT into markdown (stdout), as kept in
-profiles/paged_decode_<CONFIG>.md; for c4 also OUT/traffic.json, the per-launch HBM traffic that
-bench.py reports as roofline.traffic (profiles/traffic_c4_decode.json).
+profiles/paged_decode_<CONFIG>.md, and write OUT/traffic.json: the kernel's name, its per-launch HBM
+traffic and L2 hit rate, which bench.py --config CONFIG reports as roofline.traffic and
+roofline.tcc_hit_rate (kept as profiles/traffic_<CONFIG>.json) when the kernel it launches has that
+name.
 
 Dispatches of one `bench.py --no-extras` run, in order: the library's set-up fill, the flush
 buffer's 1 GiB fill, then (1 GiB flush read, paged_decode) per step, warm-up steps first. The
@@ -176,12 +178,12 @@ def main(cfg, out):
     print("## Per-workgroup timeline (measurement build with workgroup timestamps, build-ts/)\n")
     with open(os.path.join(out, "timeline.md")) as f:
         print(f.read().strip())
-    if cfg == "c4":
-        with open(os.path.join(out, "traffic.json"), "w") as f:
-            json.dump({"kernel": f"paged_decode f16 c4 (fused): {kname}", "bytes_per_launch": round(traffic),
-                       "fetch_kib": fetch_kib, "write_kib": write_kib, "fetch_factor": f_factor,
-                       "write_factor": w_factor, "tcc_hit_rate": round(dec_hit, 4),
-                       "source": "paged_decode_c4.md"}, f, indent=1)
+    with open(os.path.join(out, "traffic.json"), "w") as f:
+        json.dump({"config": cfg, "kernel_name": kname, "bytes_per_launch": round(traffic),
+                   "algorithmic_bytes": round(algo), "fetch_kib": fetch_kib, "write_kib": write_kib,
+                   "fetch_factor": f_factor, "write_factor": w_factor, "tcc_hit_rate": round(dec_hit, 4),
+                   "trace_avg_us": round(avg, 2), "bench_us_per_step": line["us_per_step"],
+                   "env": line.get("env"), "source": f"paged_decode_{cfg}.md"}, f, indent=1)
 
 
 if __name__ == "__main__":

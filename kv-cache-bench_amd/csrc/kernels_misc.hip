@@ -230,12 +230,21 @@ __global__ __launch_bounds__(kReadBwThreads) void read_bw_kernel(const u32x4_t* 
     if (acc == 0x9e3779b9u) sink[((size_t)blockIdx.x * T + threadIdx.x) % kReadBwSink] = 1.0f;
 }
 
+// Does nothing: the dispatch floor of a launch (kvb_run_empty_grid). The argument keeps the kernel
+// signature of a real launch (one kernarg).
+__global__ void empty_kernel(int) {}
+
 __global__ __launch_bounds__(256) void fill_kernel(uint4* dst, size_t n16, uint32_t value) {
     const uint4 v = make_uint4(value, value, value, value);
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256) dst[i] = v;
 }
 
 }  // namespace
+
+hipError_t launch_empty(int groups, int threads, hipStream_t s, const Marks& m) {
+    launch_marked(empty_kernel, dim3(groups), dim3(threads), s, m, 0);
+    return hipGetLastError();
+}
 
 hipError_t launch_paged_reduce(int head_dim, const ReduceParams& p, int batch, hipStream_t s, const Marks& m) {
     const dim3 grid(p.num_heads, batch);

@@ -158,6 +158,10 @@ struct NaiveParams {
 struct Marks {
     hipEvent_t start = nullptr;
     hipEvent_t stop = nullptr;
+    // Set: the paged_decode dispatch writes the name of the kernel it would launch here (as the
+    // profilers print it) and launches nothing.
+    char* describe = nullptr;
+    size_t describe_cap = 0;
 };
 
 template <typename... KArgs, typename... Args>
@@ -231,5 +235,7 @@ hipError_t launch_read_bw(const void* src, size_t n16, int groups, float* sink, 
                           bool nontemporal = true);
 // Overwrites n16 16-byte words with `value`.
 hipError_t launch_fill(void* dst, size_t n16, uint32_t value, hipStream_t s);
+// A kernel that does nothing, `groups` workgroups of `threads` threads (kvb_run_empty_grid).
+hipError_t launch_empty(int groups, int threads, hipStream_t s, const Marks& m);
 
 }  // namespace kvbk

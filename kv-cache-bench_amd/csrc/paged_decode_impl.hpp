@@ -48,6 +48,7 @@
 #pragma once
 
 #include <algorithm>
+#include <cstdio>
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -1175,6 +1176,14 @@ hipError_t loads_only_lds(size_t* lds) {
 
 template <int KIND, int D, int QG, bool FAST, bool PAIR, bool PART, bool SHARE, bool STAGE = false>
 hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Marks& m) {
+    if (m.describe) {  // the demangled name of the instantiation below, as rocprofv3 prints it
+        auto tf = [](bool x) { return x ? "true" : "false"; };
+        const bool loads = FAST && p.loads_only;
+        std::snprintf(m.describe, m.describe_cap,
+                      "void kvbk::paged_decode_kernel<%d, %d, %d, %s, %s, %s, %s, %s, %s>(kvbk::DecodeParams)", KIND, D,
+                      QG, tf(FAST), tf(loads), tf(PAIR), tf(PART), tf(SHARE), tf(!loads && STAGE));
+        return hipSuccess;
+    }
     const int gz = PAIR ? (p.max_parts + 1) / 2 : p.max_parts;
     const dim3 grid(p.num_heads / p.qg, p.ragged_items ? p.ragged_items : batch, p.ragged_items ? 1 : gz);
     if (p.loads_only) {  // tile-aligned pages only

@@ -287,6 +287,7 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     if (fused) {
         p.out = a->out;
         if (counters) p.counters = counters;
+        else if (mk.step.describe) p.counters = nullptr;  // (nothing is launched)
         else if (int st = counters_for(a, &p.counters)) return st;
     }
     const bool fast = a->page_size % kvbk::kTile == 0 && part % kvbk::kTile == 0;
@@ -304,7 +305,8 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     const long long nb_max = span % a->page_size == 0 ? span / a->page_size : span / a->page_size + 2;
     p.table_in_lanes = fast && nb_max <= kvbk::kLaneBlocks;
     p.table_in_lds = !fast && nb_max <= kvbk::kTableStage;
-    const kvbk::Marks dm{mk.step.start ? mk.step.start : mk.decode.start, fused ? mk.step.stop : mk.decode.stop};
+    const kvbk::Marks dm{mk.step.start ? mk.step.start : mk.decode.start, fused ? mk.step.stop : mk.decode.stop,
+                         mk.step.describe, mk.step.describe_cap};
     const kvbk::Marks rm{mk.reduce.start, mk.step.stop ? mk.step.stop : mk.reduce.stop};
     hipError_t e = hipSuccess;
     switch (a->kv_type) {
@@ -313,6 +315,13 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
         default: e = kvbk::launch_paged_decode_i8(a->head_dim, qg, fast, p, a->batch, g.stream, dm); break;
     }
     if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("paged_decode launch: ") + hipGetErrorString(e));
+    if (mk.step.describe) {
+        if (!fused && !loads_only) {
+            const size_t n = std::strlen(mk.step.describe);
+            std::snprintf(mk.step.describe + n, mk.step.describe_cap - n, " + paged_reduce");
+        }
+        return KVB_OK;
+    }
     if (fused || loads_only) return KVB_OK;
     kvbk::ReduceParams r{part_out, part_ml, a->seq_lens, a->out, a->num_heads, p.max_parts, part, p.len_cap};
     e = kvbk::launch_paged_reduce(a->head_dim, r, a->batch, g.stream, rm);
@@ -354,6 +363,57 @@ int kvb_device_name(char* buf, size_t cap) {
     else
         std::snprintf(buf, cap, "%s, %d CUs", prop.gcnArchName, prop.multiProcessorCount);
     return KVB_OK;
+}
+
+int kvb_device_info(kvb_device_info_t* info) {
+    if (!info) return fail(KVB_EINVAL, "null kvb_device_info_t");
+    *info = kvb_device_info_t{};
+    if (int st = ensure_device()) return st;
+    KVB_HIP(hipRuntimeGetVersion(&info->runtime_version));
+    KVB_HIP(hipDriverGetVersion(&info->driver_version));
+    hipDeviceProp_t prop;
+    KVB_HIP(hipGetDeviceProperties(&prop, g.device));
+    std::snprintf(info->name, sizeof(info->name), "%s", prop.name);
+    std::snprintf(info->arch, sizeof(info->arch), "%s", prop.gcnArchName);
+    KVB_HIP(hipDeviceGetPCIBusId(info->pci_bus_id, sizeof(info->pci_bus_id), g.device));
+    info->device = g.device;
+    info->compute_units = prop.multiProcessorCount;
+    KVB_HIP(hipDeviceGetAttribute(&info->clock_khz, hipDeviceAttributeClockRate, g.device));
+    KVB_HIP(hipDeviceGetAttribute(&info->memory_clock_khz, hipDeviceAttributeMemoryClockRate, g.device));
+    KVB_HIP(hipDeviceGetAttribute(&info->memory_bus_bits, hipDeviceAttributeMemoryBusWidth, g.device));
+    KVB_HIP(hipDeviceGetAttribute(&info->l2_bytes, hipDeviceAttributeL2CacheSize, g.device));
+    info->total_memory = prop.totalGlobalMem;
+    size_t free_b = 0, total_b = 0;
+    KVB_HIP(hipMemGetInfo(&free_b, &total_b));
+    info->free_memory = free_b;
+    return KVB_OK;
+}
+
+int kvb_paged_kernel_name(const kvb_paged_args* a, int loads_only, char* buf, size_t cap) {
+    if (!buf || cap == 0) return fail(KVB_EINVAL, "null buffer");
+    buf[0] = '\0';
+    if (int st = validate_paged(a)) return st;
+    if (loads_only && (a->page_size % kvbk::kTile != 0 || resolve_part(a) % kvbk::kTile != 0))
+        return fail(KVB_EINVAL, "the loads-only decode needs page_size and part_tokens that are multiples of 16");
+    if (int st = ensure_device()) return st;
+    if (a->batch == 0) return KVB_OK;
+    StepMarks mk;
+    mk.step.describe = buf;
+    mk.step.describe_cap = cap;
+    return enqueue_paged(a, nullptr, nullptr, !loads_only, mk, loads_only != 0);
+}
+
+int kvb_run_empty_grid(int workgroups, int threads, double* ms) {
+    if (ms) *ms = 0.0;
+    if (workgroups < 1 || threads < 1 || threads > 1024 || threads % 64 != 0)
+        return fail(KVB_EINVAL, "kvb_run_empty_grid: workgroups >= 1 and threads a multiple of 64 up to 1024");
+    if (int st = ensure_device()) return st;
+    hipEvent_t e0, e1;
+    if (int st = get_event(&e0)) return st;
+    if (int st = get_event(&e1)) return st;
+    const hipError_t e = kvbk::launch_empty(workgroups, threads, g.stream, {e0, e1});
+    if (e != hipSuccess) return fail(KVB_ERUNTIME, std::string("empty grid launch: ") + hipGetErrorString(e));
+    return finish(e0, e1, ms);
 }
 
 const char* kvb_last_error(void) { return g_err.c_str(); }

@@ -140,7 +140,7 @@ int mi355x_part_tokens(const Shape& s, std::span<const int> lens, int min_groups
 }
 
 int ragged_part_cap(int max_len) {
-    if (max_len >= 8 * kRaggedLongCap) return kRaggedLongCap;
+    if (max_len >= 7 * kRaggedLongCap) return kRaggedLongCap;
     return max_len >= 2 * kRaggedCap ? kRaggedCap : kRaggedShortCap;
 }
 

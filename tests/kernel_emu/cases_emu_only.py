@@ -59,3 +59,48 @@ def test_device_lengths_that_disagree_stay_in_bounds(emu, kv, page, part, host_l
             np.testing.assert_array_equal(dev.output(), fresh, err_msg=f"the step after device lengths {lens}")
     finally:
         dev.free()
+
+
+@pytest.mark.parametrize("kv", ["f16", "i8"])
+def test_graph_replay_with_device_lengths_that_disagree(emu, kv):
+    """A captured graph keeps the grid and the work order that the host's lengths gave at capture.
+    Ragged (lengths not all equal): device lengths that make a different number of work items turn
+    every replay into a no-op (the output keeps what it held), and the replay after the lengths agree
+    again gives the bits of a fresh step. Plain (equal lengths at capture): shorter device lengths are
+    clamped and served like an eager step with the same device lengths."""
+    kvb = emu
+    part = 16
+    for host_lens, dev_lens in (((40, 17), (40, 40)), ((40, 40), (17, 40))):
+        w = kvb.Workload(kvb.Shape(2, 8, 2, 64), kv, list(host_lens), seed=7, q_amp=2.0, varied=(kv == "i8"))
+        dev = kvb.DeviceCase(w, kvb.PagedCache(w, 16, 9, pool_factor=1.5, poison=True))
+        graph = None
+        try:
+            dev.out.fill(0xFF)
+            dev.run(part)
+            fresh = dev.output()
+            graph = dev.capture_graph(part, 1)
+            dev.out.fill(0xFF)
+            graph.launch()
+            np.testing.assert_array_equal(dev.output(), fresh)
+            dev.lens.upload(np.array(dev_lens, np.int32))
+            if host_lens[0] != host_lens[1]:
+                dev.out.fill(0x7F)
+                before = dev.output()
+                graph.launch()
+                np.testing.assert_array_equal(dev.output(), before, err_msg="a disagreeing ragged replay wrote")
+            else:
+                dev.out.fill(0xFF)
+                dev.run(part)
+                eager = dev.output()
+                dev.out.fill(0xFF)
+                graph.launch()
+                np.testing.assert_array_equal(dev.output(), eager)
+                assert not np.array_equal(eager[0], fresh[0])
+            dev.lens.upload(np.asarray(w.lens, np.int32))
+            dev.out.fill(0xFF)
+            graph.launch()
+            np.testing.assert_array_equal(dev.output(), fresh, err_msg="the replay after the lengths agree again")
+        finally:
+            if graph is not None:
+                graph.free()
+            dev.free()

@@ -365,8 +365,30 @@ hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t a, int d) {
         case hipDeviceAttributeMultiprocessorCount: *v = 256; return hipSuccess;
         case hipDeviceAttributeMaxSharedMemoryPerMultiprocessor: *v = 160 * 1024; return hipSuccess;
         case hipDeviceAttributeMaxSharedMemoryPerBlock: *v = 64 * 1024; return hipSuccess;
+        case hipDeviceAttributeClockRate: *v = 0; return hipSuccess;  // (no clock: not a GPU)
+        case hipDeviceAttributeMemoryClockRate: *v = 0; return hipSuccess;
+        case hipDeviceAttributeMemoryBusWidth: *v = 0; return hipSuccess;
+        case hipDeviceAttributeL2CacheSize: *v = 0; return hipSuccess;
     }
     return hipErrorInvalidValue;
+}
+// The emulation's own version numbers: 0 stands for "no HIP runtime".
+hipError_t hipRuntimeGetVersion(int* v) {
+    *v = 0;
+    return hipSuccess;
+}
+hipError_t hipDriverGetVersion(int* v) {
+    *v = 0;
+    return hipSuccess;
+}
+hipError_t hipDeviceGetPCIBusId(char* buf, int len, int d) {
+    if (d != 0) return hipErrorInvalidDevice;
+    std::snprintf(buf, size_t(len), "emulated");
+    return hipSuccess;
+}
+hipError_t hipMemGetInfo(size_t* free_bytes, size_t* total_bytes) {
+    *free_bytes = *total_bytes = size_t(1) << 34;
+    return hipSuccess;
 }
 hipError_t hipDeviceSynchronize() { return hipSuccess; }
 hipError_t hipMalloc(void** p, size_t bytes) {

@@ -529,6 +529,10 @@ enum hipDeviceAttribute_t {
     hipDeviceAttributeMultiprocessorCount = 1,
     hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
     hipDeviceAttributeMaxSharedMemoryPerBlock,
+    hipDeviceAttributeClockRate,
+    hipDeviceAttributeMemoryClockRate,
+    hipDeviceAttributeMemoryBusWidth,
+    hipDeviceAttributeL2CacheSize,
 };
 enum hipStreamCaptureMode { hipStreamCaptureModeGlobal = 0, hipStreamCaptureModeThreadLocal, hipStreamCaptureModeRelaxed };
 constexpr unsigned hipStreamNonBlocking = 1;
@@ -563,6 +567,10 @@ hipError_t hipGetDevice(int* d);
 hipError_t hipSetDevice(int d);
 hipError_t hipGetDeviceProperties(hipDeviceProp_t* p, int d);
 hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t a, int d);
+hipError_t hipRuntimeGetVersion(int* v);
+hipError_t hipDriverGetVersion(int* v);
+hipError_t hipDeviceGetPCIBusId(char* buf, int len, int d);
+hipError_t hipMemGetInfo(size_t* free_bytes, size_t* total_bytes);
 hipError_t hipDeviceSynchronize();
 hipError_t hipMalloc(void** p, size_t bytes);
 template <class T>

@@ -84,3 +84,41 @@ def test_bench_line_contract(kvb):
     cpu = d["cpu_baseline"]
     assert cpu["value"] > 0 and cpu["cores"] >= 1 and cpu["kind"] in ("reference", "port")
     assert cpu["sample"].startswith("the whole step")
+    env = d["env"]
+    assert env["hip_runtime_version"] > 0 and env["compute_units"] > 0 and len(env["loadavg_before"]) == 3
+    assert env["commit"] and env["sources_sha256"] and env["cpu_threads"] >= 1
+    assert rf["kernel"].startswith("void kvbk::paged_decode_kernel<")
+    if rf["traffic"] is not None:  # a record measured on this very kernel
+        assert rf["traffic_source"] == "profiles/traffic_c1.json"
+
+
+def test_traffic_record_needs_the_same_kernel(tmp_path, monkeypatch):
+    """bench.py attaches profiles/traffic_<config>.json only when it was measured on the kernel the run
+    launches; a record for another instantiation, or none at all, gives null with the reason."""
+    import json
+    bench = load_bench()
+    k = "void kvbk::paged_decode_kernel<1, 128, 4, true, false, true, false, false, false>(kvbk::DecodeParams)"
+    os.makedirs(tmp_path / "profiles")
+    with open(tmp_path / "profiles" / "traffic_c2.json", "w") as f:
+        json.dump({"config": "c2", "kernel_name": k, "bytes_per_launch": 135000000, "tcc_hit_rate": 0.34}, f)
+    monkeypatch.setattr(bench, "ROOT", str(tmp_path))
+    rec, why = bench.traffic_record("c2", k)
+    assert why is None and rec["bytes_per_launch"] == 135000000 and rec["tcc_hit_rate"] == 0.34
+    rec, why = bench.traffic_record("c2", k.replace("true, false, true", "true, false, false"))
+    assert rec is None and "was measured on" in why
+    rec, why = bench.traffic_record("c3", k)
+    assert rec is None and why.startswith("no profiles/traffic_c3.json")
+
+
+def test_env_record_names_the_build():
+    """The build's source identity (build/build_info.json, written by the package Makefile) matches
+    the sources as they are, and names a commit; a GPU run adds the device and HIP versions."""
+    import json
+    bench = load_bench()
+    bi = bench.build_info
+    with open(bi.BUILD_INFO) as f:
+        built = json.load(f)
+    assert set(built) >= {"commit", "dirty", "sources_sha256", "built_at", "hipcc"}
+    assert built["sources_sha256"] == bi.sources_sha256()
+    assert bi.cpu_threads() >= 1 and bi.cpu_model()
+    assert bench.cpu_threads() == bi.cpu_threads()

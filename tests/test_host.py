@@ -85,14 +85,14 @@ def test_mi355x_partition_policy(kvb):
     assert kvb.mi355x_part_tokens(kvb.Shape(16, 32, 8, 128), 8192) == 4096
     assert kvb.mi355x_part_tokens(kvb.Shape(16, 32, 8, 128), 8192, min_groups=512) == 2048
     # a ragged batch (lengths not all equal) caps the partition at 2048 while its longest sequence is
-    # under 2 x 3584 tokens, 4096 from 8 x 4096, 3584 between: c5's lengths -> 3584; c4's equal
+    # under 2 x 3584 tokens, 4096 from 7 x 4096, 3584 between: c5's lengths -> 3584; c4's equal
     # lengths keep 4096; the cap yields to a larger min_part; an all-empty batch gets the floor
     c5 = kvb.Shape(72, 32, 8, 128)
     assert max(kvb.c5_lengths()) >= 2 * 3584
     assert kvb.mi355x_part_tokens_for(c5, kvb.c5_lengths()) == 3584
     assert kvb.mi355x_part_tokens_for(c5, kvb.c5_lengths(), min_part=4096) == 4096
     s64 = kvb.Shape(64, 32, 8, 128)
-    for longest, cap in ((4096, 2048), (7167, 2048), (7168, 3584), (32767, 3584), (32768, 4096), (65536, 4096)):
+    for longest, cap in ((4096, 2048), (7167, 2048), (7168, 3584), (28671, 3584), (28672, 4096), (65536, 4096)):
         lens = [100] * 63 + [longest]
         assert kvb.mi355x_part_tokens_for(s64, lens) == cap, (longest, cap)
     assert kvb.mi355x_part_tokens_for(kvb.Shape(4, 64, 8, 128), [32768] * 4) == 4096
@@ -103,6 +103,26 @@ def test_mi355x_partition_policy(kvb):
     # BASELINE names c1's and c2's partitions; the policy is used where it leaves the choice
     assert kvb.CONFIGS["c1"]["part"] == 128 and kvb.CONFIGS["c2"]["part"] == 512
     assert all(kvb.CONFIGS[n]["part"] == "mi355x" for n in ("c3", "c4", "c5f16", "c5i8"))
+
+
+# The ragged batches the cap was measured on (32 q / 8 KV heads, head_dim 128, page 64): B lengths
+# ~U[1, L] drawn with numpy's default_rng, three from seed 5 and three from seed 11 in this order,
+# with each batch's longest sequence and token count as drawn, and the partition that ran fastest of
+# 2048 / 3584 / 4096 on MI355X (fp16 and int8 agree; 128 x U[1, 8192] is the one batch where the
+# cap's 3584 is not the fastest: 4096 was 1.1% faster in fp16).
+RAGGED_BATCHES = (
+    (5, ((64, 4096, 4093, 127111, 2048), (64, 8192, 8032, 260108, 3584), (64, 32768, 32496, 1089010, 4096))),
+    (11, ((32, 16384, 16295, 269525, 3584), (128, 8192, 8163, 520274, 3584), (16, 65536, 65478, 615616, 4096))),
+)
+
+
+def test_ragged_cap_on_the_measured_batches(kvb):
+    for seed, batches in RAGGED_BATCHES:
+        rng = np.random.default_rng(seed)
+        for B, L, longest, tokens, want in batches:
+            lens = [int(x) for x in rng.integers(1, L + 1, size=B)]
+            assert (max(lens), sum(lens)) == (longest, tokens), (seed, B, L)  # the same draw as measured
+            assert kvb.mi355x_part_tokens_for(kvb.Shape(B, 32, 8, 128), lens) == want, (B, L)
 
 
 class TestRefusals:

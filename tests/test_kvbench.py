@@ -55,6 +55,8 @@ def test_kvbench_accuracy(gpu):
     out = subprocess.run([KVBENCH, "--accuracy", "--batch=2", "--lens=300,1000", "--pages=16,64"],
                          capture_output=True, text=True, timeout=300)
     assert out.returncode == 0, out.stderr
+    env = [ln for ln in out.stdout.splitlines() if ln.startswith("# env ")]
+    assert len(env) == 1 and "hip_runtime=" in env[0] and " hip_runtime=0 " not in env[0], env
     head, body = csv_rows(out.stdout)
     assert ",".join(head) == REFERENCE_HEADERS["accuracy"][0]
     assert len(body) == 2 * 2 * 3 * 2  # data x lens x types x pages

@@ -68,3 +68,18 @@ def test_noalloc_refusals(gpu):
         assert np.array_equal(dev.output(), before, equal_nan=True)
     finally:
         dev.free()
+    # more (sequence, head) pairs than the scratch has counters: 130 x 128 = 16640 > 16384, with a
+    # workspace (one partition each) well inside the scratch
+    w = kvb.Workload(kvb.Shape(130, 128, 16, 64), "f16", [1] * 130, seed=4)
+    dev = kvb.DeviceCase(w, kvb.PagedCache(w, 16, 5))
+    try:
+        assert dev.workspace_bytes(16) < (16 << 20)
+        dev.out.fill(0x7F)
+        before = dev.output()
+        a = dev.args(16)
+        assert kvb.hip.kvb_run_paged_noalloc(ctypes.byref(a)) == kvb.KVB_EINVAL
+        err = kvb.hip.kvb_last_error()
+        assert b"KVB_NOALLOC_MAX_GROUPS" in err and b"16640" in err, err
+        assert np.array_equal(dev.output(), before, equal_nan=True)
+    finally:
+        dev.free()
