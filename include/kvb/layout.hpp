@@ -65,15 +65,39 @@ inline size_t paged_index(const Shape& s, const PagedLayout& L, int b, int kvh, 
     return ((blk * s.num_kv_heads + kvh) * L.page_size + t % L.page_size) * s.head_dim + d;
 }
 
+// One page of one KV head of one sequence: the `rows` live tokens from token t0 of sequence b (t0 a
+// multiple of the page size), held in physical block `block`. Its rows are one contiguous run in both
+// layouts: from contig_index(b, kvh, t0, 0) in the contiguous cache, from row 0 of (block, kvh) in the
+// pool. The cache writers below work slice by slice.
+struct PageSlice {
+    int b, kvh, t0, rows;
+    int32_t block;
+    size_t elems(const Shape& s) const { return size_t(rows) * s.head_dim; }
+    size_t contig_at(const Shape& s, int max_len) const { return contig_index(s, max_len, b, kvh, t0, 0); }
+    size_t paged_at(const Shape& s, const PagedLayout& L) const {
+        return (size_t(block) * s.num_kv_heads + kvh) * L.page_size * s.head_dim;
+    }
+};
+
+// Calls fn(PageSlice) for every live (sequence, logical block, KV head), sequences in order.
+template <class Fn>
+void for_each_page_slice(const Shape& s, const PagedLayout& L, std::span<const int> seq_lens, Fn&& fn) {
+    for (int b = 0; b < s.batch; ++b) {
+        const int32_t* blocks = L.block_table.data() + size_t(b) * L.max_blocks;
+        for (int t0 = 0; t0 < seq_lens[b]; t0 += L.page_size) {
+            const int rows = std::min(L.page_size, seq_lens[b] - t0);
+            for (int kvh = 0; kvh < s.num_kv_heads; ++kvh) fn(PageSlice{b, kvh, t0, rows, blocks[t0 / L.page_size]});
+        }
+    }
+}
+
 // Copies every live token of the contiguous cache into the pool (src/reference.hpp:60-68).
 template <class T>
 void scatter_to_paged(const Shape& s, const PagedLayout& L, std::span<const int> seq_lens, int max_len,
                       const T* contig, T* paged) {
-    for (int b = 0; b < s.batch; ++b)
-        for (int kvh = 0; kvh < s.num_kv_heads; ++kvh)
-            for (int t = 0; t < seq_lens[b]; ++t)
-                std::copy_n(contig + contig_index(s, max_len, b, kvh, t, 0), s.head_dim,
-                            paged + paged_index(s, L, b, kvh, t, 0));
+    for_each_page_slice(s, L, seq_lens, [&](const PageSlice& p) {
+        std::copy_n(contig + p.contig_at(s, max_len), p.elems(s), paged + p.paged_at(s, L));
+    });
 }
 
 // int8 storage: the live page_size x D values of one (physical block, KV head) become int8 with one

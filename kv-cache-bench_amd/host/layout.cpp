@@ -1,6 +1,7 @@
 // Paged layout, int8 quantiser and pool poisoning of the host layer (src/reference.cpp:11-63).
 #include "kvb/layout.hpp"
 
+#include <algorithm>
 #include <cstring>
 #include <numeric>
 #include <stdexcept>
@@ -31,49 +32,49 @@ PagedLayout make_paged_layout(std::span<const int> seq_lens, int page_size, uint
     std::mt19937_64 g(seed);
     for (long long i = pool - 1; i > 0; --i) std::swap(phys[size_t(i)], phys[rng::below(g(), uint64_t(i) + 1)]);
 
+    // the shuffled ids are handed out in sequence order, a run of ceil(len / page) per sequence
     L.block_table.assign(seq_lens.size() * size_t(L.max_blocks), -1);
-    size_t next = 0;
+    auto next = phys.cbegin();
     for (size_t b = 0; b < seq_lens.size(); ++b) {
-        const int blocks = (seq_lens[b] + page_size - 1) / page_size;
-        for (int i = 0; i < blocks; ++i) L.block_table[b * L.max_blocks + i] = phys[next++];
+        const auto run = (seq_lens[b] + page_size - 1) / page_size;
+        std::copy(next, next + run, L.block_table.begin() + std::ptrdiff_t(b * size_t(L.max_blocks)));
+        next += run;
     }
     return L;
 }
 
+namespace {
+
+// The reference's rounding of one value (src/reference.cpp:44-47): IEEE division, round half to
+// even, clamp to +-127; a zero scale (an all-zero slice) stores 0.
+int8_t quantize_one(float x, float scale) {
+    return scale > 0 ? int8_t(std::clamp(std::nearbyint(x / scale), -127.0f, 127.0f)) : int8_t(0);
+}
+
+// max |x| over a slice; a NaN never becomes the running value (std::max keeps its first argument).
+float slice_amax(std::span<const float> x) {
+    return std::accumulate(x.begin(), x.end(), 0.0f, [](float m, float v) { return std::max(m, std::fabs(v)); });
+}
+
+}  // namespace
+
 void quantize_to_paged_i8(const Shape& s, const PagedLayout& L, std::span<const int> seq_lens, int max_len,
                           const float* contig, int8_t* paged, float* scales) {
-    const int P = L.page_size, D = s.head_dim;
-    for (int b = 0; b < s.batch; ++b)
-        for (int i = 0; i * P < seq_lens[b]; ++i)
-            for (int kvh = 0; kvh < s.num_kv_heads; ++kvh) {
-                const int t0 = i * P, t1 = std::min(seq_lens[b], t0 + P);
-                float amax = 0;
-                for (int t = t0; t < t1; ++t) {
-                    const float* row = contig + contig_index(s, max_len, b, kvh, t, 0);
-                    for (int d = 0; d < D; ++d) amax = std::max(amax, std::fabs(row[d]));
-                }
-                const float scale = amax / 127.0f;
-                scales[size_t(L.block_table[size_t(b) * L.max_blocks + i]) * s.num_kv_heads + kvh] = scale;
-                for (int t = t0; t < t1; ++t) {
-                    const float* row = contig + contig_index(s, max_len, b, kvh, t, 0);
-                    int8_t* dst = paged + paged_index(s, L, b, kvh, t, 0);
-                    for (int d = 0; d < D; ++d)
-                        dst[d] = scale > 0 ? int8_t(std::clamp(std::nearbyint(row[d] / scale), -127.0f, 127.0f)) : 0;
-                }
-            }
+    for_each_page_slice(s, L, seq_lens, [&](const PageSlice& p) {
+        const std::span<const float> x(contig + p.contig_at(s, max_len), p.elems(s));
+        const float scale = slice_amax(x) / 127.0f;
+        scales[size_t(p.block) * s.num_kv_heads + p.kvh] = scale;
+        std::transform(x.begin(), x.end(), paged + p.paged_at(s, L), [scale](float v) { return quantize_one(v, scale); });
+    });
 }
 
 void dequantize_paged_i8(const Shape& s, const PagedLayout& L, std::span<const int> seq_lens, int max_len,
                          const int8_t* paged, const float* scales, float* contig) {
-    for (int b = 0; b < s.batch; ++b)
-        for (int kvh = 0; kvh < s.num_kv_heads; ++kvh)
-            for (int t = 0; t < seq_lens[b]; ++t) {
-                const float scale =
-                    scales[size_t(L.block_table[size_t(b) * L.max_blocks + t / L.page_size]) * s.num_kv_heads + kvh];
-                const int8_t* src = paged + paged_index(s, L, b, kvh, t, 0);
-                float* dst = contig + contig_index(s, max_len, b, kvh, t, 0);
-                for (int d = 0; d < s.head_dim; ++d) dst[d] = float(src[d]) * scale;
-            }
+    for_each_page_slice(s, L, seq_lens, [&](const PageSlice& p) {
+        const float scale = scales[size_t(p.block) * s.num_kv_heads + p.kvh];
+        const int8_t* q = paged + p.paged_at(s, L);
+        std::transform(q, q + p.elems(s), contig + p.contig_at(s, max_len), [scale](int8_t v) { return float(v) * scale; });
+    });
 }
 
 void poison_paged(const Shape& s, const PagedLayout& L, std::span<const int> seq_lens, size_t elem_size, void* paged,
