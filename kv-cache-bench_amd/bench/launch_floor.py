@@ -5,6 +5,9 @@ stamped by the dispatches. Run it under `rocprofv3 --kernel-trace --stats` to se
 as the profiler times them.
 
 usage: python3 kv-cache-bench_amd/bench/launch_floor.py [--reps N]
+       python3 kv-cache-bench_amd/bench/launch_floor.py --trace DIR   (summarise DIR/run_kernel_trace.csv,
+           a rocprofv3 --kernel-trace of the first form: each kernel and grid, dispatched right after the
+           flush (cold) or not (warm), with the profiler's durations)
 """
 from __future__ import annotations
 
@@ -28,10 +31,41 @@ def timed(kvb, fn, reps, cold):
     return statistics.median(out), min(out)
 
 
+def summarise_trace(out):
+    """Median profiler duration per (kernel, workgroups, cold/warm), in dispatch order of first use."""
+    import csv
+    rows = sorted(csv.DictReader(open(os.path.join(out, "run_kernel_trace.csv"))), key=lambda r: int(r["Dispatch_Id"]))
+    groups, order, prev = {}, [], None
+    for i, r in enumerate(rows):
+        name = r["Kernel_Name"]
+        if "paged_decode_kernel" in name and i + 1 < len(rows) and "paged_reduce" in rows[i + 1]["Kernel_Name"]:
+            name += " [two-kernel form]"
+        wgs = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]) // (
+            int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"]))
+        dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        flush = "read_bw_kernel<false>" in name
+        if not flush and "fill_kernel" not in name and "copyBuffer" not in name:
+            key = (name, wgs, int(r["Workgroup_Size_X"]), "cold" if prev == "flush" else "warm")
+            if key not in groups:
+                groups[key] = []
+                order.append(key)
+            groups[key].append(dur)
+        prev = "flush" if flush or (prev == "flush" and "[two-kernel form]" in name) else "other"
+    print("| kernel | workgroups x threads | in a cold step (after the flush) | dispatches | median us | min us |")
+    print("|---|---|---|---|---|---|")
+    for key in order:
+        v = groups[key]
+        print(f"| `{key[0]}` | {key[1]} x {key[2]} | {'yes' if key[3] == 'cold' else 'no'} | "
+              f"{len(v)} | {statistics.median(v):.2f} | {min(v):.2f} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--reps", type=int, default=30)
+    ap.add_argument("--trace", default=None)
     args = ap.parse_args()
+    if args.trace:
+        return summarise_trace(args.trace)
     kvb = graft.load_package()
     if not kvb.gpu_available():
         sys.exit("no GPU")

@@ -10,7 +10,8 @@ namespace {
 constexpr float kNegBigR = -1e30f;
 
 // Merges the partitions of one (sequence, query head) (src/kernels.metal:123-147): weights
-// l_i * exp(m_i - M) over the ceil(len / part) written slots; an empty sequence gives exactly 0.
+// l_i * exp(m_i - M) over the ceil(len / part) written slots; an empty sequence gives exactly 0, and
+// a sequence of one partition takes that partition's output as it is.
 // Grid (H, B), D threads: each thread owns one output element.
 template <int D>
 __global__ __launch_bounds__(D) void paged_reduce_kernel(ReduceParams p) {
@@ -22,6 +23,10 @@ __global__ __launch_bounds__(D) void paged_reduce_kernel(ReduceParams p) {
         return;
     }
     const size_t base = ((size_t)b * H + h) * p.max_parts;
+    if (parts == 1) {  // one partition: its normalised output is the output (the fused step writes it so)
+        o[d] = p.part_out[base * D + d];
+        return;
+    }
     float M = kNegBigR;
     for (int i = 0; i < parts; ++i) M = fmaxf(M, p.part_ml[base + i].x);
     float L = 0.0f, acc = 0.0f;
@@ -31,7 +36,7 @@ __global__ __launch_bounds__(D) void paged_reduce_kernel(ReduceParams p) {
         L += w;
         acc = __builtin_fmaf(w, p.part_out[(base + i) * D + d], acc);
     }
-    o[d] = acc / L;
+    o[d] = acc * (1.0f / L);  // (the fused merge normalises the same way: the same bits)
 }
 
 template <int KIND>

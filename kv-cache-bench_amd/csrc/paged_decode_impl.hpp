@@ -49,6 +49,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <type_traits>
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -61,6 +62,7 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef int i32x2_t __attribute__((ext_vector_type(2)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
@@ -85,12 +87,15 @@ constexpr int kNonTemporal = 2;
 
 #ifdef KVB_WG_TIMESTAMPS
 // Measurement build only (make -C kv-cache-bench_amd timestamps, into build-ts/): per-workgroup
-// s_memrealtime stamps (100 MHz) of the last launch, kWgStampWords per linear workgroup id: start,
-// wave 0's loop end, partition stored and acknowledged (loop end again for the loads-only variant),
-// merge done (0 where the workgroup did not merge), and where wave 0 ran: HW_ID (SIMD, CU, SH, SE) in
-// the low 32 bits, XCC_ID above. Read by kvb_wg_stamps_<kind> (paged_decode_<kind>.hip). The stamped
-// build waits for its partition stores before the merge test in the two-kernel form too.
-constexpr unsigned kWgStampGroups = 65536, kWgStampWords = 5;
+// s_memrealtime stamps (100 MHz) of the last launch, kWgStampWords per linear workgroup id:
+//   0 start; 1 wave 0's loop end; 2 the slowest wave's loop end; 3 the partition stores issued (after
+//   the wave states are merged); 4 those stores acknowledged; 5 the arrival count returned (0 in the
+//   two-kernel form); 6 merge done (0 where the workgroup did not merge); 7 where wave 0 ran: HW_ID
+//   (SIMD, CU, SH, SE) in the low 32 bits, XCC_ID above.
+// The loads-only variant writes its loop end into words 1-4. Read by kvb_wg_stamps_<kind>
+// (paged_decode_<kind>.hip). The stamped build waits for its partition stores before the merge test
+// in the two-kernel form too.
+constexpr unsigned kWgStampGroups = 65536, kWgStampWords = 8;
 __device__ unsigned long long g_wg_stamps[kWgStampGroups * kWgStampWords];
 __device__ __forceinline__ unsigned long long wg_where() {
     const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);    // hwreg(HW_REG_HW_ID)
@@ -106,6 +111,10 @@ __device__ __forceinline__ float dpp(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
 }
 constexpr int kQuadSwap1 = 0xB1;  // quad_perm [1,0,3,2]: lane l <-> l ^ 1
+// The value of lane l ^ 1 (every lane of a quad permutation is valid: no old value to keep).
+__device__ __forceinline__ float quad_swap1(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), kQuadSwap1, 0xF, 0xF, true));
+}
 
 // The max / sum of a value over lanes l, l^16, l^32, l^48, on every lane. (Not v_permlane16/32_swap:
 // with the same value in both operands this compiler folds the two results into one.)
@@ -203,15 +212,6 @@ struct TileRegs {
 };
 
 // ---- the kernel ---------------------------------------------------------------------------------
-
-// Relaxed agent-scope accesses: on gfx950 these are global_store/global_load with sc1, coherent
-// across the XCDs' L2s for this one location without flushing the caches.
-__device__ __forceinline__ void store_agent(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_agent(float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // ---- longest-first work order for ragged batches ---------------------------------------------
 // With DecodeParams::ragged_items set, grid y enumerates work items rather than (sequence,
@@ -353,14 +353,15 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     constexpr int kKvPolicy = SHARE ? 0 : kNonTemporal;
 
     // Per wave: the V tile (32 rows of D elements, swizzled); after the loop it holds the wave's
-    // final accumulators [QG][D] fp32 for the merge: the larger of the two (QG 16 int8: the
-    // accumulators).
-    constexpr int SVB = kTok * T::LDS_ESZ >= QG * 4 ? kTok * D * T::LDS_ESZ : QG * D * 4;
+    // final accumulators [8 HB][D] fp32 for the merge (every head column of a head block is written,
+    // the ones past qg unread): the larger of the two.
+    constexpr int SVB = kTok * T::LDS_ESZ >= 8 * HB * 4 ? kTok * D * T::LDS_ESZ : 8 * HB * D * 4;
     __shared__ __attribute__((aligned(16))) unsigned char s_v[W][SVB];
     __shared__ float2 s_ml[W][QG];
     // PAIR: each wave's state for the first partition, [QG][D] fp32 and (m, l), as the V tile holds
-    // the last partition's after the walk
-    __shared__ __attribute__((aligned(16))) float s_part[PAIR ? W : 1][PAIR ? QG * D : 4];
+    // the last partition's after the walk (room for 8 heads at least: state_to_lds writes all 8 of a
+    // head block, the heads past qg unread)
+    __shared__ __attribute__((aligned(16))) float s_part[PAIR ? W : 1][PAIR ? (QG > 8 ? QG : 8) * D : 4];
     __shared__ float2 s_ml2[PAIR ? W : 1][QG];
 
     // Grid (H / qg, B, max_parts), head group fastest: workgroups go to the 8 XCDs round robin by
@@ -881,23 +882,27 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // score (p = 0, corr = 1 exactly), reads zeros or masked rows, and at most renormalises the
     // int8 accumulators by a power of two, so it changes nothing. (sched_barrier: the scheduler
     // would otherwise move part of the prefetch across the wait or below the computation.)
-    // ---- the wave's state -> LDS: [QG][D] fp32 (a high-column lane (hl == 0) holds d = 16 mb +
-    // 4 q4 + i (i < 4) of head hh, one 16-byte chunk per mb; chunk c of head h's row is stored at
-    // c ^ (h & 7) so that the 8 heads' rows do not all start in the same LDS banks) and (m, l).
-    // `live`: false writes an empty state (a wave with no tile in that partition).
+    // ---- the wave's state -> LDS: [8 HB][D] fp32 and (m, l). The lanes of column pair (2 hh, 2 hh + 1)
+    // hold the high and low parts of d = 16 mb + 4 q4 + i (i < 4) of head hh; their sums form one
+    // 16-byte chunk per mb, of which lane hl writes values 2 hl and 2 hl + 1 (no lane idles and no
+    // branch splits the swaps from the adds). Chunk c of head h's row is stored at c ^ (h & 7) so that
+    // the 8 heads' rows do not all start in the same LDS banks. Heads past qg (PART, or QG 4 and less)
+    // are written too and never read. `live`: false writes an empty state (a wave with no tile in
+    // that partition).
     auto state_to_lds = [&](float* dst, float2* dml, bool live) {
         const float vupf = KIND == KV_I8 ? ldexpf(1.0f, ve) : 1.0f;
         for (int hb = 0; hb < HB; ++hb) {
             const int hq = 8 * hb + hh;  // the workgroup's head of this lane's column
             const float lsum = sum_x16_x32(l[hb]);
             for (int mb = 0; mb < NMB; ++mb) {
-                float4 o4;  // high + low columns
-                o4.x = (acc[hb][mb][0] + dpp<kQuadSwap1>(acc[hb][mb][0])) * vupf;
-                o4.y = (acc[hb][mb][1] + dpp<kQuadSwap1>(acc[hb][mb][1])) * vupf;
-                o4.z = (acc[hb][mb][2] + dpp<kQuadSwap1>(acc[hb][mb][2])) * vupf;
-                o4.w = (acc[hb][mb][3] + dpp<kQuadSwap1>(acc[hb][mb][3])) * vupf;
-                if (!live) o4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                if (hl == 0 && qcol[hb]) *reinterpret_cast<float4*>(dst + hq * D + 4 * ((4 * mb + q4) ^ (hq & 7))) = o4;
+                // lane hl keeps values 2 hl, 2 hl + 1 and sends the other two, which its partner
+                // (lane l ^ 1, the other part) keeps
+                const floatx4_t a = acc[hb][mb];
+                const float k0 = hl ? a[2] : a[0], k1 = hl ? a[3] : a[1];
+                const float x0 = hl ? a[0] : a[2], x1 = hl ? a[1] : a[3];
+                float2 v = make_float2(k0 + quad_swap1(x0), k1 + quad_swap1(x1));
+                v = live ? make_float2(v.x * vupf, v.y * vupf) : make_float2(0.0f, 0.0f);
+                *reinterpret_cast<float2*>(dst + hq * D + 4 * ((4 * mb + q4) ^ (hq & 7)) + 2 * hl) = v;
             }
             if (hl == 0 && qcol[hb] && q4 == 0) dml[hq] = live ? make_float2(m[hb], lsum) : make_float2(kNegBig, 0.0f);
         }
@@ -935,13 +940,14 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
 
 #ifdef KVB_WG_TIMESTAMPS
     const unsigned long long ts1 = __builtin_amdgcn_s_memrealtime();
+    __shared__ unsigned long long s_loop_end[W];
+    if (lane == 0) s_loop_end[wave] = ts1;
     if (LOADS && threadIdx.x == 0 && lin < kWgStampGroups) {
         unsigned long long* st = g_wg_stamps + kWgStampWords * lin;
         st[0] = ts0;
-        st[1] = ts1;
-        st[2] = ts1;
-        st[3] = 0;
-        st[4] = wg_where();
+        st[1] = st[2] = st[3] = st[4] = ts1;
+        st[5] = st[6] = 0;
+        st[7] = wg_where();
     }
 #endif
     if constexpr (LOADS) {  // (never true for real data; keeps the loads live)
@@ -962,6 +968,10 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     }
     state_to_lds(sacc, s_ml[wave], last_live);
     __syncthreads();
+#ifdef KVB_WG_TIMESTAMPS
+    unsigned long long ts_slowest = 0;
+    for (int w = 0; w < W; ++w) ts_slowest = s_loop_end[w] > ts_slowest ? s_loop_end[w] : ts_slowest;
+#endif
 
     // The partition's result: thread e owns the 16-byte chunk ed of head eh. It weighs the waves'
     // states once, sums them in wave order, and writes the chunk with one agent-scope (sc1) store,
@@ -990,30 +1000,35 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
             o.z = __builtin_fmaf(v.z, wt, o.z);
             o.w = __builtin_fmaf(v.w, wt, o.w);
         }
-        const float4 r = make_float4(o.x / L, o.y / L, o.z / L, o.w / L);
+        const float inv = 1.0f / L;  // (one division; L >= 1: the partition holds a live token)
+        const float4 r = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
         const size_t slot0 = ((size_t)b * H + h0) * p.max_parts + part + gp;  // head h0's slot
         const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(
             p.part_out + slot0 * D, (short)0, NQ * p.max_parts * D * 4, 0x00020000);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, r), rpo,
                                                (eh * p.max_parts * D + 4 * ed) * 4, 0, kScopeAgent);
-        if (ed == 0) {
-            const size_t slot = slot0 + (size_t)eh * p.max_parts;
-            store_agent(&p.part_ml[slot].x, M * kLn2);
-            store_agent(&p.part_ml[slot].y, L);
+        if (ed == 0) {  // (m, l) as one 8-byte agent-scope store
+            const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(
+                p.part_ml + slot0, (short)0, NQ * p.max_parts * 8, 0x00020000);
+            const u32x2_t ml = {__builtin_bit_cast(uint32_t, M * kLn2), __builtin_bit_cast(uint32_t, L)};
+            __builtin_amdgcn_raw_buffer_store_b64(ml, rml, eh * p.max_parts * 8, 0, kScopeAgent);
         }
         if (p.out && len <= p.part_tokens)  // one partition: this is the output
             *reinterpret_cast<float4*>(p.out + ((size_t)b * H + h0 + eh) * D + 4 * ed) = r;
       }
     }
 #ifdef KVB_WG_TIMESTAMPS
+    const unsigned long long ts_issued = __builtin_amdgcn_s_memrealtime();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (threadIdx.x == 0 && lin < kWgStampGroups) {
         unsigned long long* st = g_wg_stamps + kWgStampWords * lin;
         st[0] = ts0;
         st[1] = ts1;
-        st[2] = __builtin_amdgcn_s_memrealtime();
-        st[3] = 0;
-        st[4] = wg_where();
+        st[2] = ts_slowest;
+        st[3] = ts_issued;
+        st[4] = __builtin_amdgcn_s_memrealtime();
+        st[5] = st[6] = 0;
+        st[7] = wg_where();
     }
 #endif
     if (!p.out || len <= p.part_tokens) return;
@@ -1035,6 +1050,9 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     if (threadIdx.x == 0)
         s_last = __hip_atomic_fetch_add(counter, ng, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nparts - ng;
     __syncthreads();
+#ifdef KVB_WG_TIMESTAMPS
+    if (threadIdx.x == 0 && lin < kWgStampGroups) g_wg_stamps[kWgStampWords * lin + 5] = __builtin_amdgcn_s_memrealtime();
+#endif
     if (!s_last) return;
 
     // The merge is on the step's critical path (it starts when the last partition ends), so its
@@ -1056,6 +1074,13 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                               rpo, ((eh * p.max_parts + i) * D + 4 * ed) * 4, 0, kScopeAgent));
     };
+    const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(p.part_ml + gbase, (short)0,
+                                                                         NQ * p.max_parts * 8, 0x00020000);
+    // (m_i, l_i) of the group's head eh, one 8-byte agent-scope load. (The vector is cast whole: this
+    // compiler's __builtin_bit_cast of an ext_vector element, v[1], gives the bits of v[0].)
+    auto ml_at = [&](int eh, int i) {
+        return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rml, (eh * p.max_parts + i) * 8, 0, kScopeAgent));
+    };
     auto add = [](float4& o, float& L, float wt, const float4& v) {
         L += wt;
         o.x = __builtin_fmaf(wt, v.x, o.x);
@@ -1063,36 +1088,42 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         o.z = __builtin_fmaf(wt, v.z, o.z);
         o.w = __builtin_fmaf(wt, v.w, o.w);
     };
-    auto write_out = [&](int ec, const float4& o, float L) {
+    auto write_out = [&](int ec, const float4& o, float L) {  // (paged_reduce's normalisation)
         const int eh = ec / (D / 4), ed = ec % (D / 4);
+        const float inv = 1.0f / L;
         *reinterpret_cast<float4*>(p.out + ((size_t)b * H + h0 + eh) * D + 4 * ed) =
-            make_float4(o.x / L, o.y / L, o.z / L, o.w / L);
+            make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
     };
-    if (nparts <= kPre) {  // uniform
-        // Up to kPre partitions (every BASELINE configuration): each owner reads its head's (m_i, l_i)
-        // straight from the workspace together with its rows, so the merge is one round trip with
-        // no barrier. Same weights, same order as below.
+    // Up to kPre partitions (every BASELINE configuration): each owner reads its head's (m_i, l_i)
+    // straight from the workspace together with its rows, so the merge is one round trip with no
+    // barrier. Same weights, same order as below. N: a bound on nparts known at compile time (8 covers
+    // the BASELINE configurations and halves the code the merge walks through).
+    auto merge_few = [&](auto bound) {
+        constexpr int N = decltype(bound)::value;
         for (int ec = threadIdx.x; ec < NQ * D / 4; ec += 64 * W) {
-            float4 pre[kPre];
-            float2 ml[kPre];
-            const size_t mslot = gbase + (size_t)(ec / (D / 4)) * p.max_parts;
-            for (int j = 0; j < kPre; ++j)
+            float4 pre[N];
+            float2 ml[N];
+            for (int j = 0; j < N; ++j)
                 if (j < nparts) {
                     pre[j] = row(ec, j);
-                    ml[j] = make_float2(load_agent(&p.part_ml[mslot + j].x), load_agent(&p.part_ml[mslot + j].y));
+                    ml[j] = ml_at(ec / (D / 4), j);
                 }
             float M = kNegBig;
-            for (int j = 0; j < kPre; ++j)
+            for (int j = 0; j < N; ++j)
                 if (j < nparts) M = fmaxf(M, ml[j].x);
             float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             float L = 0.0f;
-            for (int j = 0; j < kPre; ++j)
+            for (int j = 0; j < N; ++j)
                 if (j < nparts) add(o, L, partition_weight(ml[j].x, ml[j].y, M), pre[j]);
             write_out(ec, o, L);
         }
+    };
+    if (nparts <= kPre) {  // uniform
+        if (nparts <= 8) merge_few(std::integral_constant<int, 8>{});
+        else merge_few(std::integral_constant<int, kPre>{});
         if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef KVB_WG_TIMESTAMPS
-        if (threadIdx.x == 0 && lin < kWgStampGroups) g_wg_stamps[kWgStampWords * lin + 3] = __builtin_amdgcn_s_memrealtime();
+        if (threadIdx.x == 0 && lin < kWgStampGroups) g_wg_stamps[kWgStampWords * lin + 6] = __builtin_amdgcn_s_memrealtime();
 #endif
         return;
     }
@@ -1103,10 +1134,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         const bool owner = ec < NQ * D / 4;
         float4 pre[kPre];
         for (int j = 0; j < kPre; ++j) pre[j] = row(ec, j);
-        for (int x = threadIdx.x; x < NQ * nparts; x += 64 * W) {
-            const size_t slot = gbase + (size_t)(x / nparts) * p.max_parts + x % nparts;
-            s_pml[x] = make_float2(load_agent(&p.part_ml[slot].x), load_agent(&p.part_ml[slot].y));
-        }
+        for (int x = threadIdx.x; x < NQ * nparts; x += 64 * W) s_pml[x] = ml_at(x / nparts, x % nparts);
         __syncthreads();
         for (int x = threadIdx.x; x < NQ * nparts; x += 64 * W) {
             const float2* mrow = s_pml + (x / nparts) * nparts;
@@ -1131,7 +1159,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     }
     if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef KVB_WG_TIMESTAMPS
-    if (threadIdx.x == 0 && lin < kWgStampGroups) g_wg_stamps[kWgStampWords * lin + 3] = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0 && lin < kWgStampGroups) g_wg_stamps[kWgStampWords * lin + 6] = __builtin_amdgcn_s_memrealtime();
 #endif
 }
 

@@ -575,7 +575,7 @@ static void model_partition(const split_job* j, int b, int h, int part) {
     for (int d = 0; d < D; ++d) {
         float o = 0.0f;
         for (int w = 0; w < j->waves; ++w) o += wacc[w][d] * wt[w];
-        j->ws_out[slot * D + d] = o / L;
+        j->ws_out[slot * D + d] = o * (1.0f / L); /* the kernel multiplies by one reciprocal */
     }
     j->ws_ml[2 * slot] = M;
     j->ws_ml[2 * slot + 1] = L;
@@ -597,6 +597,10 @@ static void model_reduce(const split_job* j, int b, int h) {
     }
     const float* ml = j->ws_ml + 2 * row * j->max_parts;
     const float* po = j->ws_out + row * j->max_parts * D;
+    if (parts == 1) { /* one partition: its normalised output is the output */
+        for (int d = 0; d < D; ++d) out[d] = po[d];
+        return;
+    }
     float M = -INFINITY;
     for (int i = 0; i < parts; ++i)
         if (ml[2 * i] > M) M = ml[2 * i];
@@ -607,7 +611,7 @@ static void model_reduce(const split_job* j, int b, int h) {
             L += w;
             o += w * po[(size_t)i * D + d];
         }
-        out[d] = o / L;
+        out[d] = o * (1.0f / L);
     }
 }
 

@@ -267,6 +267,16 @@ inline void raw_buffer_store_b128(u32x4_emu v, BufferRsrc r, int voffset, int so
     const uint32_t d[4] = {v[0], v[1], v[2], v[3]};
     buffer_write(r, voffset, soffset, d, 4);
 }
+typedef uint32_t u32x2_emu __attribute__((ext_vector_type(2)));
+inline u32x2_emu raw_buffer_load_b64(BufferRsrc r, int voffset, int soffset, int /*aux*/) {
+    uint32_t d[2];
+    buffer_read(r, voffset, soffset, d, 2);
+    return u32x2_emu{d[0], d[1]};
+}
+inline void raw_buffer_store_b64(u32x2_emu v, BufferRsrc r, int voffset, int soffset, int /*aux*/) {
+    const uint32_t d[2] = {v[0], v[1]};
+    buffer_write(r, voffset, soffset, d, 2);
+}
 
 // ---- cross-lane operations --------------------------------------------------------------------------
 constexpr uint64_t op_key(uint64_t op, uint64_t a = 0, uint64_t b = 0) { return (op << 56) ^ (a << 24) ^ b; }
@@ -302,6 +312,12 @@ T update_dpp(T old, T src, int ctrl, int row_mask, int bank_mask, bool bound_ctr
                                   else outs[l] = ins[s].src;
                               }
                           });
+}
+// mov_dpp: update_dpp with no old value (the kernels use it with every row and bank enabled, where the
+// old value is never taken; elsewhere it stands in as 0).
+template <class T>
+T mov_dpp(T src, int ctrl, int row_mask, int bank_mask, bool bound_ctrl) {
+    return update_dpp(T{}, src, ctrl, row_mask, bank_mask, bound_ctrl);
 }
 template <class T>
 T shfl_xor(T v, int mask, int width) {
@@ -494,7 +510,10 @@ typedef ::kvbemu::BufferRsrc __amdgpu_buffer_rsrc_t;
 #define __builtin_amdgcn_raw_buffer_load_b128 ::kvbemu::raw_buffer_load_b128
 #define __builtin_amdgcn_raw_buffer_load_b32 ::kvbemu::raw_buffer_load_b32
 #define __builtin_amdgcn_raw_buffer_store_b128 ::kvbemu::raw_buffer_store_b128
+#define __builtin_amdgcn_raw_buffer_load_b64 ::kvbemu::raw_buffer_load_b64
+#define __builtin_amdgcn_raw_buffer_store_b64 ::kvbemu::raw_buffer_store_b64
 #define __builtin_amdgcn_update_dpp ::kvbemu::update_dpp
+#define __builtin_amdgcn_mov_dpp ::kvbemu::mov_dpp
 #define __builtin_amdgcn_readlane ::kvbemu::readlane
 #define __builtin_amdgcn_readfirstlane ::kvbemu::readfirstlane
 #define __builtin_amdgcn_ballot_w64 ::kvbemu::ballot

@@ -104,6 +104,7 @@ __global__ void dpp_kernel(int* out) {
     out[192 + l] = __shfl_xor(l, 5);
     out[256 + l] = __builtin_amdgcn_readlane(l * 3, 17);
     out[320 + l] = (int)(__ballot(l % 3 == 0) >> (l % 32) & 1);
+    out[384 + l] = __builtin_amdgcn_mov_dpp(7 * l + 1, 0xB1, 0xF, 0xF, true);  // no old value
 }
 
 template <class T>
@@ -197,11 +198,11 @@ int main() {
         check(ok, "ds_read_b64_tr_b8: lane i of a 16-lane group gets column i of the 8 rows its group addresses");
     }
     {
-        Dev<int> out(384);
+        Dev<int> out(448);
         hipLaunchKernelGGL(dpp_kernel, dim3(1), dim3(64), 0, 0, out.d);
         bool ok = launched();
         out.down();
-        bool shr = ok, scan = ok, xr = ok, rl = ok, bal = ok;
+        bool shr = ok, scan = ok, xr = ok, rl = ok, bal = ok, mov = ok;
         for (int l = 0; l < 64; ++l) {
             ok = ok && out.h[l] == (l ^ 1);
             shr = shr && out.h[64 + l] == (l % 16 == 0 ? -1 : l - 1);
@@ -209,6 +210,7 @@ int main() {
             xr = xr && out.h[192 + l] == (l ^ 5);
             rl = rl && out.h[256 + l] == 51;
             bal = bal && out.h[320 + l] == (int)(((l % 32) % 3 == 0));
+            mov = mov && out.h[384 + l] == 7 * (l ^ 1) + 1;
         }
         check(ok, "DPP quad_perm [1,0,3,2]");
         check(shr, "DPP row_shr:1 keeps the old value in each row's first lane");
@@ -216,6 +218,7 @@ int main() {
         check(xr, "__shfl_xor");
         check(rl, "v_readlane");
         check(bal, "ballot");
+        check(mov, "mov_dpp quad_perm [1,0,3,2] (bound_ctrl, no old value)");
     }
     std::printf("%s: %d failure(s)\n", g_failures ? "FAILED" : "PASSED", g_failures);
     return g_failures ? 1 : 0;

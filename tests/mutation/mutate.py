@@ -110,7 +110,7 @@ MUTANTS = [
       "vs[i] = j->v_scale[blk * Hkv + kvh];", "vs[i] = j->k_scale[blk * Hkv + kvh];"),
     K("int8: V scale of the sequence's first block for every block",
       "vs[i] = j->v_scale[blk * Hkv + kvh];", "vs[i] = j->v_scale[(size_t)bt[0] * Hkv + kvh];"),
-    K("partition merge never writes the output", "out[d] = o / L;", "(void)o;"),
+    K("partition merge never writes the output", "out[d] = o * (1.0f / L);", "(void)o;"),
     K("partition merge takes one partition too many at an exact multiple",
       "int parts = (model_len(j, b) + j->part_tokens - 1) / j->part_tokens;",
       "int parts = model_len(j, b) / j->part_tokens + 1;"),
@@ -186,7 +186,7 @@ MUTANTS = [
     X("wave merge reads the other waves' rows without their swizzle",
       "wacc(w) + eh * D + 4 * (ed ^ (eh & 7)));", "wacc(w) + eh * D + 4 * ed);"),
     X("partition output not divided by its sum",
-      "const float4 r = make_float4(o.x / L, o.y / L, o.z / L, o.w / L);",
+      "const float4 r = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);",
       "const float4 r = make_float4(o.x, o.y, o.z, o.w);"),
     X("fused merge counts only the full partitions",
       "const int nparts = (len + p.part_tokens - 1) / p.part_tokens;", "const int nparts = len / p.part_tokens;"),
@@ -279,7 +279,7 @@ MUTANTS = [
     H("head count not a multiple of the KV heads accepted", RUNTIME, "if (H % Hkv != 0)", "if (false)"),
     H("writer: int8 without scales accepted", RUNTIME, "|| (a->kv_type == KVB_KV_I8 && !a->scales)", ""),
     H("host quantiser truncates", "kv-cache-bench_amd/host/layout.cpp",
-      "std::nearbyint(row[d] / scale)", "std::trunc(row[d] / scale)"),
+      "std::nearbyint(x / scale)", "std::trunc(x / scale)"),
     H("host layout: table entries past a sequence's blocks not -1", "kv-cache-bench_amd/host/layout.cpp",
       "L.block_table.assign(seq_lens.size() * size_t(L.max_blocks), -1);",
       "L.block_table.assign(seq_lens.size() * size_t(L.max_blocks), 0);"),
