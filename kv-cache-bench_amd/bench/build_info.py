@@ -9,7 +9,7 @@ whether the sources on the box are the ones built.
 
 `env_record(kvb)` is the environment object of a bench line: that source identity, the HIP runtime
 and driver versions and the device (kvb_device_info), the ROCm release, the CPU and the load average
-before the run.
+before the run. `python3 build_info.py --env` prints it as JSON (sweep.sh saves it as env.json).
 """
 from __future__ import annotations
 
@@ -139,6 +139,12 @@ def env_record(kvb, loadavg=None) -> dict:
 
 
 if __name__ == "__main__":
+    if sys.argv[1:] == ["--env"]:  # the environment record of a result set, now (needs the GPU library)
+        sys.path.insert(0, ROOT)
+        import __graft_entry__ as graft
+
+        sys.stdout.write(json.dumps(env_record(graft.load_package()), indent=1) + "\n")
+        sys.exit(0)
     rec = build_record()
     text = json.dumps(rec, indent=1) + "\n"
     if len(sys.argv) > 1:
