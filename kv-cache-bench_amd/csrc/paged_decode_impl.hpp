@@ -977,11 +977,15 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // states once, sums them in wave order, and writes the chunk with one agent-scope (sc1) store,
     // which writes through this XCD's L2 to the device coherence point, where the merging workgroup,
     // on whichever XCD, reads it.
-    // PAIR: the same for each of the range's partitions (the first's states in s_part).
-    // (one chunk per thread up to QG 8; QG 16 at head_dim 128: two)
-    for (int gp = 0; gp < ng; ++gp) {  // uniform
-      const bool lastp = gp == ng - 1;
-      for (int ec = threadIdx.x; ec < NQ * D / 4; ec += 64 * W) {
+    // PAIR: the same for each of the range's partitions (the first's states in s_part), both at
+    // once: item i is chunk i % CH of partition i / CH, so at QG 4 (128 chunks) the two partitions
+    // take the two halves of the workgroup instead of two rounds of half of it.
+    // (one item per thread up to QG 8 with one partition; QG 16 at head_dim 128: two)
+    const int CH = NQ * D / 4;  // chunks per partition
+    for (int item = threadIdx.x; item < ng * CH; item += 64 * W) {
+        const int gp = PAIR && item >= CH ? 1 : 0;  // (ng <= 2)
+        const bool lastp = gp == ng - 1;
+        const int ec = item - gp * CH;
         const int eh = ec / (D / 4), ed = ec % (D / 4);
         auto wml = [&](int w) { return lastp ? s_ml[w][eh] : s_ml2[PAIR ? w : 0][eh]; };
         auto wacc = [&](int w) {
@@ -1015,7 +1019,6 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
         }
         if (p.out && len <= p.part_tokens)  // one partition: this is the output
             *reinterpret_cast<float4*>(p.out + ((size_t)b * H + h0 + eh) * D + 4 * ed) = r;
-      }
     }
 #ifdef KVB_WG_TIMESTAMPS
     const unsigned long long ts_issued = __builtin_amdgcn_s_memrealtime();
