@@ -214,6 +214,20 @@ int kvb_paged_kernel_name(const kvb_paged_args* a, int loads_only, char* buf, si
 #define KVB_PAIR_OFF 1
 #define KVB_PAIR_ALWAYS 2
 int kvb_set_pair_mode(int mode);
+/* Tuning switch, not in the reference: where kvb_run_paged, kvb_run_paged_steps and the captured
+ * graph merge a step's partitions (the reference's paged_reduce, src/metal_attn.mm:184-194).
+ * KVB_MERGE_FUSED: in paged_decode itself (the last workgroup of each group merges it) wherever the
+ * fused merge can take the group; KVB_MERGE_SEPARATE: always as a second kernel, paged_reduce, which
+ * spreads the merge over a workgroup per (sequence, head). KVB_MERGE_AUTO (the default) is
+ * KVB_MERGE_FUSED: on MI355X the fused step was the faster at 8 to 64 partitions per sequence
+ * (the reference's default sweep, batch 2, 32 query / 8 KV heads: e.g. f16 at 8192 tokens, 32
+ * partitions, 20.7-21.0 us fused against 22.5 us separate). Every setting gives the same bits.
+ * Returns the previous setting, or -1 for an unknown one (nothing changed). Applies to every later
+ * decode step of the process. */
+#define KVB_MERGE_AUTO 0
+#define KVB_MERGE_FUSED 1
+#define KVB_MERGE_SEPARATE 2
+int kvb_set_merge_mode(int mode);
 
 /* ---- cache writers on the GPU --------------------------------------------------------------
  * The producers of the paged cache the decode reads, as the reference runs them on the host:

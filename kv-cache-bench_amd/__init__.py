@@ -107,6 +107,7 @@ _SIGS = {
     "kvb_run_empty_grid": ([_i, _i, _d], _i),
     "kvb_paged_kernel_name": ([_PA, _i, ctypes.c_char_p, _sz], _i),
     "kvb_set_pair_mode": ([_i], _i),
+    "kvb_set_merge_mode": ([_i], _i),
     "kvb_run_paged_noalloc": ([_PA], _i),
     "kvb_run_naive": ([_NA, _d], _i),
     "kvb_check_naive": ([_NA], _i),
@@ -579,6 +580,19 @@ def set_pair_mode(mode: str) -> str:
     if prev < 0:
         raise KvbInvalidArgument(f"set_pair_mode: unknown mode {mode!r}")
     return {v: k for k, v in PAIR_MODES.items()}[prev]
+
+
+MERGE_MODES = {"auto": 0, "fused": 1, "separate": 2}
+
+
+def set_merge_mode(mode: str) -> str:
+    """Where a decode step merges its partitions (kvb_set_merge_mode): "auto", "fused" (in
+    paged_decode, wherever it can) or "separate" (paged_reduce as a second kernel). Returns the
+    previous mode."""
+    prev = hip.kvb_set_merge_mode(MERGE_MODES[mode])
+    if prev < 0:
+        raise KvbInvalidArgument(f"set_merge_mode: unknown mode {mode!r}")
+    return {v: k for k, v in MERGE_MODES.items()}[prev]
 
 
 def set_stream(stream):

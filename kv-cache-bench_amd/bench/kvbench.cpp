@@ -5,8 +5,9 @@
 // gpu_paged_per_head, ours; layouts contiguous, paged16; err_vs stored, fp32_data), so its consumer
 // (scripts/tables.py) reads this output. Each header starts with the reference's columns; this
 // build's columns follow them. This build adds the gpu_paged_loads rows (--loads: the decode's loads
-// alone) and the flags --loads, --config, --pool, --dist, --bw-bytes, --cpu-ref and --schema (print
-// each mode's header, no GPU needed).
+// alone) and the flags --loads, --config, --pool, --dist, --bw-bytes, --cpu-ref, --merge
+// (kvb_set_merge_mode: auto, fused or separate) and --schema (print each mode's header, no GPU
+// needed).
 //
 // Modes, one per run: the sweep (default), --bw, --dump=DIR, --chain=N, --accuracy.
 // Timing: GPU time from hipEvent pairs stamped by the kernel dispatches; before each timed run a
@@ -53,6 +54,7 @@ struct Options {
     std::string dump, config, cpu_ref;
     Dist dist = Dist::uniform;
     double pool = 1.0;
+    int merge = KVB_MERGE_AUTO;  // --merge: kvb_set_merge_mode
     size_t bw_bytes = size_t(512) << 20;  // past the 256 MB MALL
 };
 
@@ -106,6 +108,12 @@ const std::vector<Flag>& flags() {
         {"--loads", false, [](Options& o, const char*) { o.loads = true; }},
         {"--config", true, [](Options& o, const char* v) { o.config = v; }},
         {"--pool", true, [](Options& o, const char* v) { o.pool = std::atof(v); }},
+        {"--merge", true,
+         [](Options& o, const char* v) {
+             o.merge = !std::strcmp(v, "fused") ? KVB_MERGE_FUSED : !std::strcmp(v, "separate") ? KVB_MERGE_SEPARATE
+                     : !std::strcmp(v, "auto")  ? KVB_MERGE_AUTO
+                                                : -1;
+         }},
         {"--dist", true, [](Options& o, const char* v) { o.dist = std::strcmp(v, "normal") ? Dist::uniform : Dist::normal; }},
         {"--bw-bytes", true, [](Options& o, const char* v) { o.bw_bytes = size_t(std::atof(v)); }},
         {"--cpu-ref", true, [](Options& o, const char* v) { o.cpu_ref = v; }},
@@ -650,8 +658,9 @@ int main(int argc, char** argv) {
         if (ch == ' ') ch = ',';
     Options o;
     if (!parse(argc, argv, o) || !apply_config(o)) return 2;
-    if (o.parts.empty() || o.reps < 1 || o.warmup < 0 || o.cpu_reps < 1) {
-        std::fprintf(stderr, "--parts needs a value; --reps and --cpu-reps at least 1, --warmup at least 0\n");
+    if (o.parts.empty() || o.reps < 1 || o.warmup < 0 || o.cpu_reps < 1 || o.merge < 0) {
+        std::fprintf(stderr, "--parts needs a value; --reps and --cpu-reps at least 1, --warmup at least 0; "
+                             "--merge is auto, fused or separate\n");
         return 2;
     }
     if (o.schema) {  // each mode's CSV header, "mode:header" (needs no GPU)
@@ -665,11 +674,13 @@ int main(int argc, char** argv) {
     }
     const int threads = int(std::max(1u, std::thread::hardware_concurrency()));
     std::printf("# device=%s batch=%d heads=%d kv_heads=%d head_dim=%d reps=%d warmup=%d cpu_reps=%d cpu_threads=%d "
-                "flush=%d simdgroups=%d timing=%s dist=%s pool=%.2f\n",
+                "flush=%d simdgroups=%d timing=%s dist=%s pool=%.2f merge=%s\n",
                 device_name().c_str(), o.shape.batch, o.shape.num_heads, o.shape.num_kv_heads, o.shape.head_dim,
                 o.reps, o.warmup, o.cpu_reps, threads, o.flush, kSimdGroups, o.sync ? "sync" : "pipelined",
-                o.dist == Dist::normal ? "normal" : "uniform", o.pool);
+                o.dist == Dist::normal ? "normal" : "uniform", o.pool,
+                o.merge == KVB_MERGE_FUSED ? "fused" : o.merge == KVB_MERGE_SEPARATE ? "separate" : "auto");
     print_env(loadavg, threads);
+    kvb_set_merge_mode(o.merge);
     const GpuTimer timer(o);
     if (o.bw) return mode_bw(o, timer);
     if (!o.dump.empty()) return mode_dump(o);

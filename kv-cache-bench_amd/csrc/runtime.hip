@@ -45,6 +45,7 @@ struct Runtime {
     hipEvent_t switch_ev = nullptr; // orders a new stream after the old one (kvb_set_stream)
     int cus = 0;                    // compute units: the read probe runs one workgroup per CU
     int pair_mode = KVB_PAIR_AUTO;  // kvb_set_pair_mode
+    int merge_mode = KVB_MERGE_AUTO;  // kvb_set_merge_mode
     float* sink = nullptr;          // read-probe sink
     bool pipelined = false;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> timed;
@@ -284,6 +285,7 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     // workgroup merge in the one-round-trip form only (at most 16 partitions)
     if (fused && qg * p.max_parts > kvbk::fused_merge_slots(a->kv_type, a->head_dim)) fused = false;
     if (fused && qg > 8 && p.max_parts > 16) fused = false;
+    if (fused && g.merge_mode == KVB_MERGE_SEPARATE) fused = false;
     if (fused) {
         p.out = a->out;
         if (counters) p.counters = counters;
@@ -436,6 +438,13 @@ int kvb_set_pair_mode(int mode) {
     if (mode != KVB_PAIR_AUTO && mode != KVB_PAIR_OFF && mode != KVB_PAIR_ALWAYS) return -1;
     const int prev = g.pair_mode;
     g.pair_mode = mode;
+    return prev;
+}
+
+int kvb_set_merge_mode(int mode) {
+    if (mode != KVB_MERGE_AUTO && mode != KVB_MERGE_FUSED && mode != KVB_MERGE_SEPARATE) return -1;
+    const int prev = g.merge_mode;
+    g.merge_mode = mode;
     return prev;
 }
 

@@ -87,8 +87,9 @@ __global__ void tr8_kernel(uint8_t* out) {
     __builtin_memcpy(&out[8 * l], &v, 8);
 }
 
-// ---- DPP: quad_perm [1,0,3,2], row_shr:1 (bound_ctrl off: lane 0 of a row keeps old), and the
-// row_bcast:15 / row_bcast:31 steps of a wave prefix sum
+// ---- DPP: quad_perm [1,0,3,2], row_shr:1 (bound_ctrl off: lane 0 of a row keeps old), the
+// row_bcast:15 / row_bcast:31 steps of a wave prefix sum, and quad_perm [2,3,0,1], row_half_mirror
+// and row_mirror (the steps of a max over 16 lanes)
 __global__ void dpp_kernel(int* out) {
     const int l = threadIdx.x;
     out[l] = __builtin_amdgcn_update_dpp(-1, l, 0xB1, 0xF, 0xF, false);
@@ -105,6 +106,9 @@ __global__ void dpp_kernel(int* out) {
     out[256 + l] = __builtin_amdgcn_readlane(l * 3, 17);
     out[320 + l] = (int)(__ballot(l % 3 == 0) >> (l % 32) & 1);
     out[384 + l] = __builtin_amdgcn_mov_dpp(7 * l + 1, 0xB1, 0xF, 0xF, true);  // no old value
+    out[448 + l] = __builtin_amdgcn_update_dpp(-1, l, 0x4E, 0xF, 0xF, false);
+    out[512 + l] = __builtin_amdgcn_update_dpp(-1, l, 0x141, 0xF, 0xF, false);
+    out[576 + l] = __builtin_amdgcn_update_dpp(-1, l, 0x140, 0xF, 0xF, false);
 }
 
 template <class T>
@@ -198,11 +202,11 @@ int main() {
         check(ok, "ds_read_b64_tr_b8: lane i of a 16-lane group gets column i of the 8 rows its group addresses");
     }
     {
-        Dev<int> out(448);
+        Dev<int> out(640);
         hipLaunchKernelGGL(dpp_kernel, dim3(1), dim3(64), 0, 0, out.d);
         bool ok = launched();
         out.down();
-        bool shr = ok, scan = ok, xr = ok, rl = ok, bal = ok, mov = ok;
+        bool shr = ok, scan = ok, xr = ok, rl = ok, bal = ok, mov = ok, q2 = ok, hm = ok, rm = ok;
         for (int l = 0; l < 64; ++l) {
             ok = ok && out.h[l] == (l ^ 1);
             shr = shr && out.h[64 + l] == (l % 16 == 0 ? -1 : l - 1);
@@ -211,6 +215,9 @@ int main() {
             rl = rl && out.h[256 + l] == 51;
             bal = bal && out.h[320 + l] == (int)(((l % 32) % 3 == 0));
             mov = mov && out.h[384 + l] == 7 * (l ^ 1) + 1;
+            q2 = q2 && out.h[448 + l] == (l ^ 2);
+            hm = hm && out.h[512 + l] == ((l & ~7) | (7 - (l & 7)));
+            rm = rm && out.h[576 + l] == ((l & ~15) | (15 - (l & 15)));
         }
         check(ok, "DPP quad_perm [1,0,3,2]");
         check(shr, "DPP row_shr:1 keeps the old value in each row's first lane");
@@ -219,6 +226,9 @@ int main() {
         check(rl, "v_readlane");
         check(bal, "ballot");
         check(mov, "mov_dpp quad_perm [1,0,3,2] (bound_ctrl, no old value)");
+        check(q2, "DPP quad_perm [2,3,0,1]");
+        check(hm, "DPP row_half_mirror");
+        check(rm, "DPP row_mirror");
     }
     std::printf("%s: %d failure(s)\n", g_failures ? "FAILED" : "PASSED", g_failures);
     return g_failures ? 1 : 0;

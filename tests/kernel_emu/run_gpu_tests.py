@@ -32,7 +32,7 @@ BUILD = os.path.join(HERE, "build")
 ASAN_BUILD = os.path.join(HERE, "build-asan")
 CXX = "/opt/rocm/lib/llvm/bin/clang++"
 
-FILES = ["tests/test_gpu_parity.py", "tests/test_gpu_groups.py", "tests/test_gpu_pair.py",
+FILES = ["tests/test_gpu_parity.py", "tests/test_gpu_groups.py", "tests/test_gpu_pair.py", "tests/test_gpu_merge.py",
          "tests/test_gpu_writer.py", "tests/test_gpu_graph.py", "tests/test_zz_no_alloc.py",
          "tests/kernel_emu/cases_emu_only.py"]  # (the last: lengths the host did not check)
 # hardware measurements, or calls into the HIP runtime itself

@@ -207,8 +207,8 @@ MUTANTS = [
       "r = WorkItem{64 * e + l, i - __builtin_amdgcn_readlane(excl, l)};",
       "r = WorkItem{64 * e + l, i + 1 - __builtin_amdgcn_readlane(excl, l)};"),
     X("paged_reduce reads partition 0's rows for every partition",
-      "acc = __builtin_fmaf(w, p.part_out[(base + i) * D + d], acc);",
-      "acc = __builtin_fmaf(w, p.part_out[base * D + d], acc);", "kv-cache-bench_amd/csrc/kernels_misc.hip"),
+      "ml[j] = p.part_ml[i];\n            v[j] = p.part_out[i * D + d];",
+      "ml[j] = p.part_ml[i];\n            v[j] = p.part_out[base * D + d];", "kv-cache-bench_amd/csrc/kernels_misc.hip"),
     X("cache writer: int8 quantiser truncates",
       "__builtin_rintf(x / scale)", "truncf(x / scale)", "kv-cache-bench_amd/csrc/cache_writer.hip"),
     # ---- the checker ----

@@ -27,6 +27,10 @@ RAGGED_LENS = [0, 1, 15, 16, 17, 63, 64, 65, 129, 300, 2, 0]
 RAGGED_LAYOUTS = [(1, 0), (3, 5), (8, 100), (16, 16), (32, 0), (48, 96), (64, 1)]
 GQA_SHAPES = [(2, 8, 8, 128), (2, 12, 4, 64), (2, 32, 2, 128), (2, 6, 2, 64)]
 MANY_PARTITIONS = [("f16", 16), ("f16", 32), ("f16", 64), ("f32", 16), ("i8", 16), ("i8", 32)]
+# head_dim 128, 4 query heads per KV head, 128-token partitions: 64 and 24 partitions per sequence,
+# the fused merge's batched form at its head_dim-128 batch size (the reference's own sweep runs 64
+# partitions at 32k tokens)
+MANY_PARTITIONS_D128 = [("f16", 128), ("f32", 128), ("i8", 128)]
 
 
 def expected(kvb, oracle, w, c):
@@ -200,14 +204,17 @@ def check_storage_bound_i8(kvb, oracle, run):
     assert oracle.max_abs_diff(got, exact) <= bound
 
 
-def many_partitions_case(kvb, kv):
+def many_partitions_case(kvb, kv, head_dim=64):
+    if head_dim == 128:
+        w = kvb.Workload(kvb.Shape(2, 32, 8, 128), kv, [8192, 3001], seed=92)
+        return w, kvb.PagedCache(w, 32, 92, pool_factor=1.25)
     w = kvb.Workload(kvb.Shape(2, 16, 2, 64), kv, [4096, 2049], seed=91)
     return w, kvb.PagedCache(w, 16, 91, pool_factor=1.25)
 
 
-def check_many_partitions(kvb, oracle, run, kv, part):
+def check_many_partitions(kvb, oracle, run, kv, part, head_dim=64):
     """Up to 256 partitions per sequence: the merge over many partitions. Returns the output."""
-    w, c = many_partitions_case(kvb, kv)
+    w, c = many_partitions_case(kvb, kv, head_dim)
     got = run(w, c, part, True)
     want, tol = expected(kvb, oracle, w, c)
     assert oracle.max_abs_diff(got, want) <= tol

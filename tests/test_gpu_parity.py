@@ -301,6 +301,19 @@ def test_many_partitions(gpu, oracle, kv, part):
     dev.free()
 
 
+@pytest.mark.parametrize("kv,part", pb.MANY_PARTITIONS_D128)
+def test_many_partitions_head_dim_128(gpu, oracle, kv, part):
+    """64 and 24 partitions at head_dim 128 (4 query heads per KV head): the fused merge's batches at
+    head_dim 128 against the oracle, and bit for bit against the two-kernel form."""
+    kvb = gpu
+    got = pb.check_many_partitions(kvb, oracle, runner(kvb), kv, part, head_dim=128)
+    w, c = pb.many_partitions_case(kvb, kv, head_dim=128)
+    dev = kvb.DeviceCase(w, c)
+    dev.run_split(part)
+    assert np.array_equal(got, dev.output())
+    dev.free()
+
+
 def test_read_bandwidth_probe(gpu):
     kvb = gpu
     buf = kvb.Buffer(1 << 30)

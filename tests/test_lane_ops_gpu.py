@@ -18,4 +18,4 @@ def test_cross_lane_operations_known_answers_on_the_gpu(gpu):
     r = subprocess.run([BIN], capture_output=True, text=True, timeout=120)
     out = r.stdout + r.stderr
     assert r.returncode == 0 and "PASSED" in out, out
-    assert out.count("ok: ") == 12, out
+    assert out.count("ok: ") == 15, out
