@@ -119,13 +119,13 @@ int kvb_paged_max_parts(const kvb_paged_args* a);
 /* Bytes of the workspace a call with these arguments uses (0 on bad arguments). */
 size_t kvb_paged_workspace_bytes(const kvb_paged_args* a);
 /* Query heads one paged_decode workgroup serves, which read each K/V page once together: with
- * share_kv, 16 when the group num_heads / num_kv_heads is a multiple of 16 and the cache is f16,
- * else the largest divisor of the group that is at most 8 (a group of 7 is one workgroup
- * per KV head, a group of 12 two of 6, a group of 32 two of 16); without share_kv, 1. The
- * reference's kernel serves the whole group from one threadgroup (QG = GROUP,
- * src/metal_attn.mm:64-80); here the score MFMA holds 8 heads and a workgroup runs one or two such
- * blocks. Returns -1 on bad arguments (num_kv_heads <= 0, num_heads not a positive multiple of it,
- * kv_type not a kvb_kv_type). */
+ * share_kv and an f16 or i8 cache, 32 or 16 when it divides the group num_heads / num_kv_heads;
+ * otherwise the largest divisor of the group that is at most 8 (a group of 7 is one workgroup per
+ * KV head, a group of 12 two of 6, a group of 64 two of 32); without share_kv, 1. The reference's
+ * kernel serves the whole group from one threadgroup (QG = GROUP, src/metal_attn.mm:64-80); here
+ * the score MFMA holds 8 heads, a wave runs one block of them (two for f16), and a workgroup of 16
+ * or 32 heads splits them over its waves, which walk the same tiles. Returns -1 on bad arguments
+ * (num_kv_heads <= 0, num_heads not a positive multiple of it, kv_type not a kvb_kv_type). */
 int kvb_heads_per_workgroup(int num_heads, int num_kv_heads, int kv_type, int share_kv);
 
 /* The refusals of kvb_run_paged alone (KVB_OK or KVB_EINVAL): reads only host_seq_lens and the
@@ -137,7 +137,8 @@ int kvb_check_paged(const kvb_paged_args* a);
  * partitions; two kernels (paged_decode, then paged_reduce) when a group's (m, l) pairs exceed what
  * that merge stages in LDS: query heads per group x max_parts > 4 waves x 32 tokens x head_dim x
  * elem_size / 8 (at head_dim 128: 4096 for f16, 8192 for f32, 2048 for i8; half that at 64), or
- * when a workgroup serves 16 query heads (kvb_heads_per_workgroup) and max_parts > 16.
+ * when max_parts > 16 and a workgroup (kvb_heads_per_workgroup) serves 16 f16 query heads, or 32
+ * heads at head_dim 128 (f16, i8), or 32 f16 heads at 64.
  * Either form gives the same bits. *ms = GPU time
  * from before the first kernel to after the last (hipEvent pair); 0 in pipelined mode. Refuses (KVB_EINVAL, before any GPU work, output untouched) part_tokens < 0, max_len < 0,
  * page_size <= 0, I8 without scales, a length < 0 or > max_len or > max_blocks * page_size,

@@ -201,9 +201,9 @@ def auto_part_tokens(batch, num_kv_heads, max_len) -> int:
 
 
 def heads_per_workgroup(shape, kv_type=KV_F16, share_kv=True) -> int:
-    """Query heads one paged_decode workgroup serves (kvb_heads_per_workgroup): 16 for a multiple of
-    16 with an f16 cache, else the largest divisor of the group that is at most 8; 1 without
-    share_kv."""
+    """Query heads one paged_decode workgroup serves (kvb_heads_per_workgroup): 32 or 16 where they
+    divide the group (f16 and i8 caches), else the largest divisor of the group that is at most 8;
+    1 without share_kv."""
     return hip.kvb_heads_per_workgroup(shape.num_heads, shape.num_kv_heads, KV_BY_NAME.get(kv_type, kv_type),
                                        int(share_kv))
 

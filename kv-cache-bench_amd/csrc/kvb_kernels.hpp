@@ -19,6 +19,37 @@ constexpr int decode_waves(int /*kind*/) { return 4; }
 // Tokens one wave handles per step of its loop: the N of a 16x16 MFMA tile.
 constexpr int kTile = 16;
 
+// The waves of a paged_decode workgroup that serves qg query heads of one KV head: qw heads per
+// wave, ts token streams (stream s walks the partition's 32-token tiles s, s + ts, ...) and hs head
+// splits (the waves of split j serve heads j * qw .. j * qw + qw - 1 and walk the same tiles as the
+// other splits' waves of their stream), hs * ts waves in all. Up to 8 heads (16 for fp16, two
+// 8-head blocks per wave) one wave serves every head: four streams, one wave per SIMD, the
+// reference's kSimdGroups. Past that the splits read each page once from HBM and again from the CU's
+// own caches, where the sibling workgroups of one KV head, each on its own CU, read it again from
+// L2 (MI355X, 4 x 32k tokens, 8 KV heads, page 128: int8 with 16 query heads per KV head 84.0 us as
+// two 8-head workgroups; fp16 with 32, 132.2 us as two 16-head workgroups; int8 with 32, 122.7 us).
+//  * int8, 16 heads: two splits of four streams, 8 waves (two per SIMD, each wave's registers as at
+//    8 heads); each split gives the bits of an 8-head workgroup.
+//  * int8, 32 heads: four splits of two streams, 8 waves.
+//  * fp16, 32 heads: two splits of two streams of 16-head waves, 4 waves (one per SIMD: a 16-head
+//    wave holds about 360 registers).
+struct DecodeShape {
+    int qw, hs, ts;
+};
+constexpr DecodeShape decode_shape(int kind, int qg) {
+    if (kind == KV_I8 && qg == 16) return DecodeShape{8, 2, 4};
+    if (kind == KV_I8 && qg == 32) return DecodeShape{8, 4, 2};
+    if (kind == KV_F16 && qg == 32) return DecodeShape{16, 2, 2};
+    return DecodeShape{qg, 1, decode_waves(kind)};
+}
+constexpr int decode_wg_waves(int kind, int qg) { return decode_shape(kind, qg).hs * decode_shape(kind, qg).ts; }
+// The fused merge of more than 16 partitions gives each thread one 16-byte chunk of the group's
+// [qg][head_dim] output; a workgroup with more chunks than threads leaves such a merge to
+// paged_reduce (fp16 workgroups of 16 heads, whose one-split build keeps that path out).
+constexpr bool fused_merge_many(int kind, int qg, int head_dim) {
+    return qg <= 8 || (decode_shape(kind, qg).hs > 1 && qg * head_dim / 4 <= 64 * decode_wg_waves(kind, qg));
+}
+
 // A sequence's length as a kernel uses it: seq_lens[b] (device memory) clamped to [0, cap], where
 // cap is what the host sized the launch for (run_paged: min(max_blocks * page_size,
 // max_parts * part_tokens); the naive kernels: max_len). The host validates its own copy of the
@@ -89,7 +120,7 @@ struct DecodeParams {
     // Nonzero: each workgroup computes two consecutive partitions (the PAIR kernels). Requires
     // tile-aligned pages, an f16 or i8 cache, the plain grid (ragged_items 0), and part_tokens a
     // multiple of 2 * kTile * decode_waves(kind) (32-token tiles, dealt round robin to the waves), so
-    // that each partition keeps its tiles' waves and order.
+    // that each partition keeps its tiles' waves and order; and one head split (decode_shape).
     int pair;
     // Query heads per workgroup: a divisor of group, at most the kernel's QG; read by the PART
     // kernels only (the others serve QG heads). Last, so that it leaves the other fields' offsets
@@ -179,9 +210,10 @@ inline void launch_marked(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipSt
 }
 
 // paged_decode for one storage kind: grid (H / qg, batch, max_parts), or (H / qg, ragged_items, 1)
-// for a ragged batch, decode_waves(kind) waves per workgroup. qg (= p.qg, 1 to 8) picks the kernel
-// built for the next of 1, 2, 4 and 8 query heads; its columns past qg are idle. `fast`: every 16-token tile lies inside one page (page_size % 16 == 0 and
-// part_tokens % 16 == 0), so block ids and scales are read once per tile.
+// for a ragged batch, decode_wg_waves(kind, qg) waves per workgroup. qg (= p.qg) picks the kernel
+// built for the next of 1, 2, 4 and 8 query heads, whose columns past qg are idle, or the one built
+// for 16 (fp16, int8) or 32 (fp16, int8) heads. `fast`: every 16-token tile lies inside one page
+// (page_size % 16 == 0 and part_tokens % 16 == 0), so block ids and scales are read once per tile.
 hipError_t launch_paged_decode_f32(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s,
                                    const Marks& m = {});
 hipError_t launch_paged_decode_f16(int head_dim, int qg, bool fast, const DecodeParams& p, int batch, hipStream_t s,

@@ -326,22 +326,32 @@ __device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int bat
 // partitions' tiles in order; each partition's tiles go to the same waves, in the same order, as in
 // a workgroup of its own (part_tokens is a multiple of 32 * waves), and a wave starts its second
 // partition from a fresh state, so every partition gets the same bits either way.
+// QG is the workgroup's query heads. Past 8 (fp16: 16) its waves split them (decode_shape: QW heads
+// per wave, HS head splits of TS token streams): a wave walks its stream's tiles for its split's
+// heads, so each tile is read by HS waves, the first from HBM and the others mostly from the CU's
+// caches, with ordinary loads.
 template <int KIND, int D, int QG, bool FAST, bool LOADS = false, bool PAIR = false, bool PART = false,
           bool SHARE = false, bool STAGE = false>
-__global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_waves_per_eu(QG > 8 ? 1 : KIND == KV_I8 && FAST && !LOADS && !PAIR && QG > 1 ? 3 : 2))) void paged_decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdgpu_waves_per_eu(
+    decode_shape(KIND, QG).qw > 8 ? 1
+    : decode_wg_waves(KIND, QG) > 4 ? 2
+    : KIND == KV_I8 && FAST && !LOADS && !PAIR && QG > 1 ? 3 : 2))) void paged_decode_kernel(DecodeParams p) {
     using T = KvT<KIND, D>;
     using R = TileRegs<KIND, D>;
-    constexpr int W = decode_waves(KIND);
+    constexpr DecodeShape DS = decode_shape(KIND, QG);
+    constexpr int QW = DS.qw, HS = DS.hs, TS = DS.ts, W = HS * TS;
     constexpr int NJ = T::NJ, VL = T::VL, NV = T::NV, NMB = D / 16;
     constexpr bool F32 = KIND == KV_F32;
-    static_assert(QG == 1 || QG == 2 || QG == 4 || QG == 8 || (QG == 16 && KIND == KV_F16),
-                  "QG must be 1, 2, 4, 8 or (fp16) 16");
+    static_assert(QG == 1 || QG == 2 || QG == 4 || QG == 8 || (QG == 16 && KIND != KV_F32) || (QG == 32 && KIND != KV_F32),
+                  "QG must be 1, 2, 4, 8 or (fp16, int8) 16 or 32");
+    static_assert(HS == 1 || (!PART && !PAIR), "head splits serve whole groups, one partition per workgroup");
+    static_assert(QW * HS == QG && (QW <= 8 || (QW == 16 && KIND == KV_F16)), "decode_shape");
     // Blocks of 8 query heads: the score MFMA's 16 columns hold 8 heads (a high and a low column
-    // each), so QG 16 runs two blocks over each tile: both read the tile's K registers and V reads.
-    // fp16 only: at c4's size with 16 query heads per KV head, fp16 ran 88.4 us this way against
-    // 106.3 us as two workgroups of 8 (SHARE); int8 ran 149.3 us against 71.4 (its arithmetic per
-    // tile, doubled, no longer hides under the loads, and its accumulators spill to AGPRs).
-    constexpr int HB = QG > 8 ? QG / 8 : 1;
+    // each), so a 16-head wave runs two blocks over each tile: both read the tile's K registers and V
+    // reads. fp16 only: at c4's size with 16 query heads per KV head, fp16 ran 88.4 us this way
+    // against 106.3 us as two workgroups of 8 (SHARE); int8 ran 149.3 us against 71.4 (its arithmetic
+    // per tile, doubled, no longer hides under the loads, and its accumulators spill to AGPRs).
+    constexpr int HB = QW > 8 ? QW / 8 : 1;
     // Tile register buffers per wave: one computed while the next is loaded (see the tile walk).
     // fp32 tiles are too large for more than one. (Three for int8, whose tiles are half an fp16
     // tile, spill at head_dim 128 and measured slower.)
@@ -350,19 +360,20 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // with SHARE, whose sibling workgroups read each page again from L2 (MI355X, c4's size with
     // groups of 16: 163.5 -> 106.9 us fp16, 88.2 -> 68.0 int8, against 133.7 / 80.9 with the sibling
     // order alone; non-temporal stays for one workgroup per KV head: 84.5 us there, 93.9 without).
-    constexpr int kKvPolicy = SHARE ? 0 : kNonTemporal;
+    // Head splits (HS > 1) read each tile once per split: ordinary loads, as SHARE.
+    constexpr int kKvPolicy = SHARE || HS > 1 ? 0 : kNonTemporal;
 
     // Per wave: the V tile (32 rows of D elements, swizzled); after the loop it holds the wave's
     // final accumulators [8 HB][D] fp32 for the merge (every head column of a head block is written,
     // the ones past qg unread): the larger of the two.
     constexpr int SVB = kTok * T::LDS_ESZ >= 8 * HB * 4 ? kTok * D * T::LDS_ESZ : 8 * HB * D * 4;
     __shared__ __attribute__((aligned(16))) unsigned char s_v[W][SVB];
-    __shared__ float2 s_ml[W][QG];
+    __shared__ float2 s_ml[W][QW];
     // PAIR: each wave's state for the first partition, [QG][D] fp32 and (m, l), as the V tile holds
     // the last partition's after the walk (room for 8 heads at least: state_to_lds writes all 8 of a
     // head block, the heads past qg unread)
-    __shared__ __attribute__((aligned(16))) float s_part[PAIR ? W : 1][PAIR ? (QG > 8 ? QG : 8) * D : 4];
-    __shared__ float2 s_ml2[PAIR ? W : 1][QG];
+    __shared__ __attribute__((aligned(16))) float s_part[PAIR ? W : 1][PAIR ? (QW > 8 ? QW : 8) * D : 4];
+    __shared__ float2 s_ml2[PAIR ? W : 1][QW];
 
     // Grid (H / qg, B, max_parts), head group fastest: workgroups go to the 8 XCDs round robin by
     // linear id, so consecutive ids (one partition of consecutive head groups and sequences) spread
@@ -419,6 +430,11 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // The wave's token stream (its tiles: stream, stream + TS, ...) and head split (its heads: hw0 ..
+    // hw0 + NQW - 1). One split: the wave's stream is its index and it serves the workgroup's heads.
+    const int stream = HS == 1 ? wave : wave % TS;
+    const int hw0 = HS == 1 ? h0 : h0 + (wave / TS) * QW;
+    const int NQW = HS == 1 ? NQ : QW;
     const int c = lane & 15, q4 = lane >> 4;  // MFMA: column (stack row of q) / token row, row quad
     // Per tile, outside the lanes case below: the block table is read through the constant address
     // space (nothing writes it during the kernel), so the wave-uniform reads are scalar loads, whose
@@ -577,7 +593,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // Head block hb's column c holds head 8 hb + c / 2.
     const int hh = c >> 1, hl = c & 1;
     bool qcol[HB];
-    for (int hb = 0; hb < HB; ++hb) qcol[hb] = 8 * hb + hh < NQ;
+    for (int hb = 0; hb < HB; ++hb) qcol[hb] = 8 * hb + hh < NQW;
     float up[HB];  // scores are MFMA results times `up` (a power of two; int8: per head)
     half8_t aq16[HB][KIND == KV_F16 ? NJ : 1];
     float aq32[F32 ? NJ : 1];
@@ -585,7 +601,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     constexpr int QS = F32 ? 1 : 8;  // q elements per MFMA slot
     float qv[HB][NJ][QS];            // raw loads only: any use before the barrier below would wait for them
     for (int hb = 0; hb < HB; ++hb) {
-        const float* qp = p.q + ((size_t)b * H + h0 + (qcol[hb] ? 8 * hb + hh : 0)) * D;
+        const float* qp = p.q + ((size_t)b * H + hw0 + (qcol[hb] ? 8 * hb + hh : 0)) * D;
         for (int j = 0; j < NJ; ++j)
             for (int s = 0; s < QS; ++s) qv[hb][j][s] = qp[T::dslot(j, q4, s)];
     }
@@ -601,10 +617,10 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     }
 
     const int ntiles = (t1 - t0 + kTok - 1) / kTok;
-    int it = wave;
+    int it = stream;
     R r[NBUF];
     for (int k = 0; k + 1 < NBUF; ++k) {
-        load_tile(r[k], t0 + (it + k * W) * kTok);
+        load_tile(r[k], t0 + (it + k * TS) * kTok);
         // (in buffer order, as the loop issues them: the loop head is entered from here and from the
         // back edge, and the wait for buffer 0 there can leave the later buffers in flight only if
         // both paths issued them in the same order)
@@ -912,13 +928,13 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // tile of the second partition the wave moves its state to s_part and starts afresh.
     int cur = 0;
     const int tpp = p.part_tokens / kTok;  // tiles per partition
-    const int wtiles = it < ntiles ? (ntiles - it + W - 1) / W : 0;
+    const int wtiles = it < ntiles ? (ntiles - it + TS - 1) / TS : 0;
     const int rounds = (wtiles + NBUF - 1) / NBUF;
     for (int rd = 0; rd < rounds; ++rd) {
 #pragma unroll
         for (int k = 0; k < NBUF; ++k) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // tile `it` (buffer k) has arrived
-            load_tile(r[(k + NBUF - 1) % NBUF], t0 + (it + (NBUF - 1) * W) * kTok);
+            load_tile(r[(k + NBUF - 1) % NBUF], t0 + (it + (NBUF - 1) * TS) * kTok);
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (PAIR && !LOADS) {
                 if (cur == 0 && it >= tpp && it < ntiles) {  // wave-uniform
@@ -934,7 +950,7 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
                 }
             }
             compute_tile(r[k], t0 + it * kTok);
-            it += W;
+            it += TS;
         }
     }
 
@@ -981,24 +997,27 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
     // once: item i is chunk i % CH of partition i / CH, so at QG 4 (128 chunks) the two partitions
     // take the two halves of the workgroup instead of two rounds of half of it.
     // (one item per thread up to QG 8 with one partition; QG 16 at head_dim 128: two)
+    // Head splits: head eh is head eh % QW of the waves of split eh / QW, whose TS streams are merged
+    // in stream order, as the TS waves of a one-split workgroup.
     const int CH = NQ * D / 4;  // chunks per partition
     for (int item = threadIdx.x; item < ng * CH; item += 64 * W) {
         const int gp = PAIR && item >= CH ? 1 : 0;  // (ng <= 2)
         const bool lastp = gp == ng - 1;
         const int ec = item - gp * CH;
         const int eh = ec / (D / 4), ed = ec % (D / 4);
-        auto wml = [&](int w) { return lastp ? s_ml[w][eh] : s_ml2[PAIR ? w : 0][eh]; };
+        const int w0 = HS == 1 ? 0 : (eh / QW) * TS, lh = HS == 1 ? eh : eh % QW;  // first wave, its head
+        auto wml = [&](int w) { return lastp ? s_ml[w0 + w][lh] : s_ml2[PAIR ? w : 0][lh]; };
         auto wacc = [&](int w) {
-            return lastp ? reinterpret_cast<const float*>(s_v[w]) : &s_part[PAIR ? w : 0][0];
+            return lastp ? reinterpret_cast<const float*>(s_v[w0 + w]) : &s_part[PAIR ? w : 0][0];
         };
         float M = kNegBig;
-        for (int w = 0; w < W; ++w) M = fmaxf(M, wml(w).x);
+        for (int w = 0; w < TS; ++w) M = fmaxf(M, wml(w).x);
         float L = 0.0f;
         float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (int w = 0; w < W; ++w) {
+        for (int w = 0; w < TS; ++w) {
             const float wt = __builtin_amdgcn_exp2f(wml(w).x - M);
             L += wml(w).y * wt;
-            const float4 v = *reinterpret_cast<const float4*>(wacc(w) + eh * D + 4 * (ed ^ (eh & 7)));
+            const float4 v = *reinterpret_cast<const float4*>(wacc(w) + lh * D + 4 * (ed ^ (lh & 7)));
             o.x = __builtin_fmaf(v.x, wt, o.x);
             o.y = __builtin_fmaf(v.y, wt, o.y);
             o.z = __builtin_fmaf(v.z, wt, o.z);
@@ -1130,9 +1149,9 @@ __global__ __launch_bounds__(64 * decode_waves(KIND)) __attribute__((amdgpu_wave
 #endif
         return;
     }
-    // More than kPre partitions: one chunk per thread, so QG <= 8 (the host leaves a QG 16 group
-    // with more than kPre partitions to paged_reduce).
-    if constexpr (QG <= 8) {
+    // More than kPre partitions: one chunk per thread (fused_merge_many; the host leaves a group with
+    // more chunks than threads and more than kPre partitions to paged_reduce).
+    if constexpr (fused_merge_many(KIND, QG, D)) {
         const int ec = threadIdx.x;
         const bool owner = ec < NQ * D / 4;
         float4 pre[kPre];
@@ -1176,7 +1195,7 @@ hipError_t loads_only_lds(size_t* lds) {
     static size_t cached = SIZE_MAX;
     if (cached == SIZE_MAX) {
         const auto loads = paged_decode_kernel<KIND, D, QG, true, true, PAIR, PART, SHARE>;
-        const int threads = 64 * decode_waves(KIND);
+        const int threads = 64 * decode_wg_waves(KIND, QG);
         int occ = 0, dev = 0, lds_cu = 0, lds_wg = 0;
         hipFuncAttributes fa{};
         hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -1223,11 +1242,11 @@ hipError_t launch_one(const DecodeParams& p, int batch, hipStream_t s, const Mar
         } else {
             size_t lds = 0;
             if (const hipError_t e = loads_only_lds<KIND, D, QG, PAIR, PART, SHARE>(&lds); e != hipSuccess) return e;
-            launch_marked_lds(paged_decode_kernel<KIND, D, QG, true, true, PAIR, PART, SHARE>, grid, dim3(64 * decode_waves(KIND)),
+            launch_marked_lds(paged_decode_kernel<KIND, D, QG, true, true, PAIR, PART, SHARE>, grid, dim3(64 * decode_wg_waves(KIND, QG)),
                               lds, s, m, p);
         }
     } else {
-        launch_marked(paged_decode_kernel<KIND, D, QG, FAST, false, PAIR, PART, SHARE, STAGE>, grid, dim3(64 * decode_waves(KIND)), s, m, p);
+        launch_marked(paged_decode_kernel<KIND, D, QG, FAST, false, PAIR, PART, SHARE, STAGE>, grid, dim3(64 * decode_wg_waves(KIND, QG)), s, m, p);
     }
     return hipGetLastError();
 }
@@ -1240,7 +1259,7 @@ hipError_t launch_qg(bool fast, const DecodeParams& p, int batch, hipStream_t s,
         return p.table_in_lds ? launch_one<KIND, D, QG, false, false, PART, SHARE, true>(p, batch, s, m)
                               : launch_one<KIND, D, QG, false, false, PART, SHARE>(p, batch, s, m);
     }
-    if constexpr (KIND != KV_F32) {
+    if constexpr (KIND != KV_F32 && decode_shape(KIND, QG).hs == 1) {
         if (p.pair) return p.ragged_items ? hipErrorInvalidValue : launch_one<KIND, D, QG, true, true, PART, SHARE>(p, batch, s, m);
     } else {
         if (p.pair) return hipErrorInvalidValue;
@@ -1267,9 +1286,14 @@ hipError_t launch_for_dim(int qg, bool fast, const DecodeParams& p, int batch, h
         case 8: return sib ? launch_qg<KIND, D, 8, false, true>(fast, p, batch, s, m)
                            : launch_qg<KIND, D, 8, false>(fast, p, batch, s, m);
         case 16:
-            if constexpr (KIND == KV_F16)
+            if constexpr (KIND != KV_F32)
                 return sib ? launch_qg<KIND, D, 16, false, true>(fast, p, batch, s, m)
                            : launch_qg<KIND, D, 16, false>(fast, p, batch, s, m);
+            return hipErrorInvalidValue;
+        case 32:
+            if constexpr (KIND != KV_F32)
+                return sib ? launch_qg<KIND, D, 32, false, true>(fast, p, batch, s, m)
+                           : launch_qg<KIND, D, 32, false>(fast, p, batch, s, m);
             return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }

@@ -281,10 +281,10 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     p.batch = a->batch;
     p.ragged_items = ragged_items(a, part);
     p.loads_only = loads_only;
-    // fused merge when the group's partition (m, l) pairs fit its LDS staging; 16 heads per
-    // workgroup merge in the one-round-trip form only (at most 16 partitions)
+    // fused merge when the group's partition (m, l) pairs fit its LDS staging; a workgroup with more
+    // output chunks than threads merges in the one-round-trip form only (at most 16 partitions)
     if (fused && qg * p.max_parts > kvbk::fused_merge_slots(a->kv_type, a->head_dim)) fused = false;
-    if (fused && qg > 8 && p.max_parts > 16) fused = false;
+    if (fused && !kvbk::fused_merge_many(a->kv_type, qg, a->head_dim) && p.max_parts > 16) fused = false;
     if (fused && g.merge_mode == KVB_MERGE_SEPARATE) fused = false;
     if (fused) {
         p.out = a->out;
@@ -299,6 +299,7 @@ int enqueue_paged(const kvb_paged_args* a, float* part_out, float2* part_ml, boo
     // tokens: 28.3 us per step, against 26.5 us for 256 workgroups of 1024 tokens).
     const long long wgs = (long long)a->batch * (a->num_heads / qg) * p.max_parts;
     p.pair = fast && a->kv_type != KVB_KV_F32 && !p.ragged_items && p.max_parts >= 2 &&
+             kvbk::decode_shape(a->kv_type, qg).hs == 1 &&
              part % (2 * kvbk::kTile * kvbk::decode_waves(a->kv_type)) == 0 &&
              (g.pair_mode == KVB_PAIR_ALWAYS || (g.pair_mode == KVB_PAIR_AUTO && wgs >= 2LL * g.cus));
     // blocks one workgroup's range touches: its tokens / page when the page divides them (the range
@@ -508,9 +509,13 @@ int kvb_heads_per_workgroup(int num_heads, int num_kv_heads, int kv_type, int sh
     if (kv_type != KVB_KV_F32 && kv_type != KVB_KV_F16 && kv_type != KVB_KV_I8) return -1;
     if (!share_kv) return 1;
     const int group = num_heads / num_kv_heads;
-    // two blocks of 8 heads: fp16 only. int8 (whose arithmetic per tile is already close to its
-    // loads) and fp32 (whose q operands are twice fp16's) run workgroups of 8.
-    if (group % 16 == 0 && kv_type == KVB_KV_F16) return 16;
+    // 32 or 16 heads (fp16, int8): one workgroup whose waves split the heads (kvbk::decode_shape),
+    // so each page is read once from HBM for the whole group. fp32 (whose q operands are twice
+    // fp16's) runs workgroups of at most 8.
+    if (kv_type != KVB_KV_F32) {
+        if (group % 32 == 0) return 32;
+        if (group % 16 == 0) return 16;
+    }
     for (int g = 8; g > 1; --g)
         if (group % g == 0) return g;
     return 1;

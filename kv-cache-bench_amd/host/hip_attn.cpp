@@ -120,7 +120,7 @@ void Buffer::mark_device_written() const { state_ = kDeviceNewer; }
 // ---- runs --------------------------------------------------------------------------------------------
 
 int mi355x_part_tokens(const Shape& s, int max_len, int min_groups, int min_part, int max_part) {
-    // (f16/i8 workgroups: a group of 16 or more may be one workgroup of 16 per KV head)
+    // (f16/i8 workgroups: a group of 16 or 32 is one workgroup per KV head)
     const int qg = std::max(1, kvb_heads_per_workgroup(s.num_heads, s.num_kv_heads, KVB_KV_F16, 1));
     const long long per_part = (long long)s.batch * (s.num_heads / qg);
     int part = max_part;

@@ -1,15 +1,19 @@
 """GQA groups other than 1, 2, 4 and 8 (3, 5, 6, 7, 9, 12, 14, 16, 32). One paged_decode workgroup serves
-kvb_heads_per_workgroup query heads of a KV head, the largest divisor of the group that is at most
-8, so it reads each K/V page once for all of them (src/metal_attn.mm:64-80 builds its kernel with
-QG = GROUP for any group). It runs the kernel built for the next of 1, 2, 4 and 8 heads, whose
-MFMA columns past those heads stay idle. Checked for every storage type:
+kvb_heads_per_workgroup query heads of a KV head: 16 or 32 where they divide the group (fp16 and
+int8), else the largest divisor of the group that is at most 8, so it reads each K/V page once for
+all of them (src/metal_attn.mm:64-80 builds its kernel with QG = GROUP for any group). Up to 8
+heads it runs the kernel built for the next of 1, 2, 4 and 8 heads, whose MFMA columns past those
+heads stay idle; 16 and 32 heads are split over the workgroup's waves. Checked for every storage
+type:
 - the output against the oracle, on the plain grid (fused merge, one and two partitions per
   workgroup), the ragged grid, and a layout whose page is not a tile multiple;
 - the fused step against the two-kernel form, bit for bit;
 - every workspace slot against the oracle's partition state;
-- groups of 16: each block of 8 heads (of the one f16 workgroup, or of the two f32 or i8
-  workgroups, which run on one XCD and read with ordinary loads) bit for bit against a group-8 run
-  of the same heads."""
+- groups of 16: each block of 8 heads (of the one f16 workgroup, of the one i8 workgroup whose
+  two head splits walk the same tiles, or of the two f32 workgroups, which run on one XCD and read
+  with ordinary loads) bit for bit against a group-8 run of the same heads;
+- 16 and 32 heads per workgroup past 16 partitions (the fused merge's many-partition form, or
+  paged_reduce where the group's output has more chunks than the workgroup has threads)."""
 import numpy as np
 import pytest
 
@@ -18,7 +22,7 @@ from conftest import progress
 
 pytestmark = pytest.mark.gpu
 
-# (B, H, Hkv, D) -> query heads per workgroup (f16; f32 and i8 caches take at most 8)
+# (B, H, Hkv, D) -> query heads per workgroup (f16 and i8; f32 caches take at most 8)
 SHAPES = [
     ((2, 24, 8, 128), 3),   # the 4-head build, one column pair idle
     ((2, 10, 2, 64), 5),    # the 8-head build from here on
@@ -27,9 +31,9 @@ SHAPES = [
     ((1, 24, 2, 128), 6),   # group 12: two workgroups per KV head
     ((1, 28, 2, 64), 7),    # group 14: two workgroups per KV head
     ((1, 18, 2, 64), 3),    # group 9: three workgroups of 3 per KV head
-    ((1, 32, 2, 128), 16),  # group 16: one workgroup of two 8-head blocks (f32, i8: two of 8)
-    ((1, 64, 2, 128), 16),  # group 32: two workgroups of 16 (f32, i8: four of 8)
-    ((2, 32, 1, 64), 16),   # group 32, one KV head, head_dim 64
+    ((1, 32, 2, 128), 16),  # group 16: f16 two 8-head blocks per wave, i8 two head splits (f32: two of 8)
+    ((1, 64, 2, 128), 32),  # group 32: f16 two splits of 16-head waves, i8 four splits (f32: four of 8)
+    ((2, 32, 1, 64), 32),   # group 32, one KV head, head_dim 64
 ]
 IDS = [f"H{s[1]}-Hkv{s[2]}-D{s[3]}" for s, _ in SHAPES]
 
@@ -59,7 +63,7 @@ def pair_restored(gpu):
 def test_groups_match_the_oracle(pair_restored, oracle, shape, qg, kv):
     kvb = pair_restored
     s = kvb.Shape(*shape)
-    qg = qg if kv == "f16" else min(qg, 8)
+    qg = qg if kv != "f32" else min(qg, 8)
     assert kvb.heads_per_workgroup(s, kv) == qg
     for kind, page, part in LAYOUTS:
         w = kvb.Workload(s, kv, lengths(kind, s.batch), seed=qg * 97 + page, varied=(kv == "i8"))
@@ -130,7 +134,8 @@ def test_groups_workspace_slots(gpu, oracle, shape, qg, kv):
 @pytest.mark.parametrize("lens,part", [([1000, 1000], 256), ([1000, 1000], 128), ([777, 65, 300, 1], 128),
                                        ([4096, 4096, 4096, 4096], 512), ([500, 300, 120], 160)])
 def test_sibling_workgroups_give_group8_bits(gpu, kv, lens, part):
-    """Group 16: f16 runs one workgroup of two 8-head blocks per KV head, f32 and i8 two workgroups
+    """Group 16: f16 runs one workgroup of two 8-head blocks per KV head, i8 one workgroup of two
+    head splits (each split's four waves walk the tiles as a group-8 workgroup's), f32 two workgroups
     of 8 (with the sibling order when the (KV head, sequence, partition) units fill blocks of 8, else
     without it). Each block of 8 heads gives the same bits as a group-8 run over the same K/V with
     those heads as the group."""
@@ -160,12 +165,16 @@ def test_sibling_workgroups_give_group8_bits(gpu, kv, lens, part):
     progress(f"[groups] group 16 = 2 x group 8 bits, {kv} lens {lens} part {part} ({units} units)")
 
 
-@pytest.mark.parametrize("kv", ["f16"])
-def test_sixteen_heads_past_sixteen_partitions(gpu, oracle, kv):
-    """A 16-head workgroup merges at most 16 partitions in the fused step; with more, the step is
-    paged_decode then paged_reduce. Against the oracle, and fused (requested) equal to two-kernel."""
+@pytest.mark.parametrize("kv", ["f16", "i8"])
+@pytest.mark.parametrize("heads,dim", [(32, 128), (64, 128), (64, 64)], ids=["g16", "g32", "g32-D64"])
+def test_wide_groups_past_sixteen_partitions(gpu, oracle, kv, heads, dim):
+    """16 and 32 heads per workgroup past 16 partitions. The fused merge of more than 16 gives each
+    thread one chunk of the group's output; a workgroup with more chunks than threads (f16 16 or 32
+    heads at head_dim 128, i8 32 heads at head_dim 128) leaves that merge to paged_reduce. Against
+    the oracle, and fused (requested) equal to two-kernel."""
     kvb = gpu
-    w = kvb.Workload(kvb.Shape(2, 32, 2, 128), kv, [1000, 333], seed=77, varied=(kv == "i8"))
+    w = kvb.Workload(kvb.Shape(2, heads, 2, dim), kv, [1000, 333], seed=77 + heads + dim, varied=(kv == "i8"))
+    assert kvb.heads_per_workgroup(w.shape, kv) == heads // 2
     c = kvb.PagedCache(w, 16, 9, pool_factor=1.5, poison=True)
     for part in (32, 64):  # 32 and 16 partitions
         dev = kvb.DeviceCase(w, c)
@@ -178,4 +187,4 @@ def test_sixteen_heads_past_sixteen_partitions(gpu, oracle, kv):
         dev.free()
         assert np.array_equal(fused.view(np.uint32), split.view(np.uint32)), part
         err = pb.check_output(kvb, oracle, w, c, fused)
-        progress(f"[groups] 16 heads, {kv}, part {part}: max err {err:.3g}")
+        progress(f"[groups] {heads // 2} heads, D {dim}, {kv}, part {part}: max err {err:.3g}")
