@@ -37,8 +37,7 @@ struct DecodeShape {
     int qw, hs, ts;
 };
 constexpr DecodeShape decode_shape(int kind, int qg) {
-    if (kind == KV_I8 && qg == 16) return DecodeShape{8, 2, 4};
-    if (kind == KV_I8 && qg == 32) return DecodeShape{8, 4, 2};
+    if (kind == KV_I8 && qg == 32) return DecodeShape{16, 2, 4};
     if (kind == KV_F16 && qg == 32) return DecodeShape{16, 2, 2};
     return DecodeShape{qg, 1, decode_waves(kind)};
 }

@@ -104,6 +104,17 @@ __device__ __forceinline__ unsigned long long wg_where() {
 }
 #endif
 
+// x as one value the compiler must materialise (an empty asm that may rewrite it). The fp16 split
+// of p into high and low parts needs the high part the P*V MFMA receives to be the one the low part
+// is taken against. For 16-head waves the compiler built the high operand with v_cvt_pk_f16_f32 from
+// the fp32 product while the low part was taken against f16(p * v_scale) rounded once by v_fma_mix:
+// on MI355X a few rows of a partition came out about one fp16 step of p off (2.3e-6 where the
+// 8-head waves of the same heads were exact).
+__device__ __forceinline__ _Float16 pinned(_Float16 x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 // ---- cross-lane helpers -------------------------------------------------------------------------
 
 template <int CTRL>
@@ -333,8 +344,8 @@ __device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int bat
 template <int KIND, int D, int QG, bool FAST, bool LOADS = false, bool PAIR = false, bool PART = false,
           bool SHARE = false, bool STAGE = false>
 __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdgpu_waves_per_eu(
-    decode_shape(KIND, QG).qw > 8 ? 1
-    : decode_wg_waves(KIND, QG) > 4 ? 2
+    decode_wg_waves(KIND, QG) > 4 ? 2
+    : decode_shape(KIND, QG).qw > 8 ? 1
     : KIND == KV_I8 && FAST && !LOADS && !PAIR && QG > 1 ? 3 : 2))) void paged_decode_kernel(DecodeParams p) {
     using T = KvT<KIND, D>;
     using R = TileRegs<KIND, D>;
@@ -345,13 +356,17 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
     static_assert(QG == 1 || QG == 2 || QG == 4 || QG == 8 || (QG == 16 && KIND != KV_F32) || (QG == 32 && KIND != KV_F32),
                   "QG must be 1, 2, 4, 8 or (fp16, int8) 16 or 32");
     static_assert(HS == 1 || (!PART && !PAIR), "head splits serve whole groups, one partition per workgroup");
-    static_assert(QW * HS == QG && (QW <= 8 || (QW == 16 && KIND == KV_F16)), "decode_shape");
-    // Blocks of 8 query heads: the score MFMA's 16 columns hold 8 heads (a high and a low column
-    // each), so a 16-head wave runs two blocks over each tile: both read the tile's K registers and V
-    // reads. fp16 only: at c4's size with 16 query heads per KV head, fp16 ran 88.4 us this way
-    // against 106.3 us as two workgroups of 8 (SHARE); int8 ran 149.3 us against 71.4 (its arithmetic
-    // per tile, doubled, no longer hides under the loads, and its accumulators spill to AGPRs).
-    constexpr int HB = QW > 8 ? QW / 8 : 1;
+    static_assert(QW * HS == QG && (QW <= 8 || (QW == 16 && KIND != KV_F32)), "decode_shape");
+    // Up to 8 heads per wave, the score MFMA's 16 columns hold each head twice (a high and a low
+    // column). With 16 heads per wave (COLH) a column holds one head: its high and low parts run as
+    // two MFMAs (int8: its three digits as three) and the P*V products as two, into separate high and
+    // low accumulators, so every lane of the softmax serves a head of its own and a 16-head tile costs
+    // the softmax instructions of an 8-head one. Same products, same sums, same order: a 16-head wave
+    // gives each head the bits of an 8-head wave. (The two-block form it replaced, two 8-head blocks
+    // per tile, ran fp16 at 4 x 32k tokens with 16 heads per KV head in 87.1 us, and int8 in 149.3.)
+    constexpr bool COLH = QW == 16;
+    constexpr int NA = COLH ? 2 : 1;      // accumulator sets: one, or (COLH) high and low
+    constexpr int HQ = COLH ? 16 : 8;     // rows of a wave's state in LDS (heads, the ones past qg unread)
     // Tile register buffers per wave: one computed while the next is loaded (see the tile walk).
     // fp32 tiles are too large for more than one. (Three for int8, whose tiles are half an fp16
     // tile, spill at head_dim 128 and measured slower.)
@@ -364,15 +379,15 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
     constexpr int kKvPolicy = SHARE || HS > 1 ? 0 : kNonTemporal;
 
     // Per wave: the V tile (32 rows of D elements, swizzled); after the loop it holds the wave's
-    // final accumulators [8 HB][D] fp32 for the merge (every head column of a head block is written,
-    // the ones past qg unread): the larger of the two.
-    constexpr int SVB = kTok * T::LDS_ESZ >= 8 * HB * 4 ? kTok * D * T::LDS_ESZ : 8 * HB * D * 4;
+    // final accumulators [HQ][D] fp32 for the merge (every head row is written, the ones past qg
+    // unread): the larger of the two.
+    constexpr int SVB = kTok * T::LDS_ESZ >= HQ * 4 ? kTok * D * T::LDS_ESZ : HQ * D * 4;
     __shared__ __attribute__((aligned(16))) unsigned char s_v[W][SVB];
     __shared__ float2 s_ml[W][QW];
     // PAIR: each wave's state for the first partition, [QG][D] fp32 and (m, l), as the V tile holds
     // the last partition's after the walk (room for 8 heads at least: state_to_lds writes all 8 of a
     // head block, the heads past qg unread)
-    __shared__ __attribute__((aligned(16))) float s_part[PAIR ? W : 1][PAIR ? (QW > 8 ? QW : 8) * D : 4];
+    __shared__ __attribute__((aligned(16))) float s_part[PAIR ? W : 1][PAIR ? HQ * D : 4];
     __shared__ float2 s_ml2[PAIR ? W : 1][QW];
 
     // Grid (H / qg, B, max_parts), head group fastest: workgroups go to the 8 XCDs round robin by
@@ -586,24 +601,24 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
                                                               rvh[h], (i * (64 / VL) + lane / VL) * D * T::ESZ + (lane % VL) * 16, 0, kKvPolicy));
     };
 
-    // ---- q as the B operand of S^T = K Q^T: column c holds head c/2, high (c even) or low part.
+    // ---- q as the B operand of S^T = K Q^T: column c holds head c/2, high (c even) or low part;
+    // COLH, head c, whose high and low parts (int8: digits) go to separate MFMAs.
     // Its loads go out first, then the wave's first NBUF - 1 tiles; the q split then runs under
     // the tiles' latency. (vmcnt counts loads in the order they were issued: a q load issued
     // after the tiles could only be waited for together with them.)
-    // Head block hb's column c holds head 8 hb + c / 2.
-    const int hh = c >> 1, hl = c & 1;
-    bool qcol[HB];
-    for (int hb = 0; hb < HB; ++hb) qcol[hb] = 8 * hb + hh < NQW;
-    float up[HB];  // scores are MFMA results times `up` (a power of two; int8: per head)
-    half8_t aq16[HB][KIND == KV_F16 ? NJ : 1];
+    const int hh = COLH ? c : c >> 1, hl = COLH ? 0 : c & 1;  // the column's head (of the wave's), its part
+    const bool qcol = hh < NQW;
+    float up;  // scores are MFMA results times `up` (a power of two; fp16: per 8 heads, int8: per head)
+    half8_t aq16[KIND == KV_F16 ? NA : 1][KIND == KV_F16 ? NJ : 1];  // COLH: high parts, low parts
     float aq32[F32 ? NJ : 1];
-    i32x4_t aq8[HB][KIND == KV_I8 ? 2 * T::KLOADS : 1];  // int8: q digits, first and second score MFMA
+    // int8: q digits of the score MFMAs (d0 + d2 and d1 + zeros; COLH: d0, d1, d2), KLOADS each
+    i32x4_t aq8[KIND == KV_I8 ? (COLH ? 3 : 2) * T::KLOADS : 1];
     constexpr int QS = F32 ? 1 : 8;  // q elements per MFMA slot
-    float qv[HB][NJ][QS];            // raw loads only: any use before the barrier below would wait for them
-    for (int hb = 0; hb < HB; ++hb) {
-        const float* qp = p.q + ((size_t)b * H + hw0 + (qcol[hb] ? 8 * hb + hh : 0)) * D;
+    float qv[NJ][QS];                // raw loads only: any use before the barrier below would wait for them
+    {
+        const float* qp = p.q + ((size_t)b * H + hw0 + (qcol ? hh : 0)) * D;
         for (int j = 0; j < NJ; ++j)
-            for (int s = 0; s < QS; ++s) qv[hb][j][s] = qp[T::dslot(j, q4, s)];
+            for (int s = 0; s < QS; ++s) qv[j][s] = qp[T::dslot(j, q4, s)];
     }
     // the partition's blocks (and int8 scales) into lanes: their round trip overlaps q's
     if (lanes) {
@@ -630,72 +645,89 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
     // their first use, and the q loads past the tiles')
     asm volatile("" ::: "memory");
 
-    for (int hb = 0; hb < HB; ++hb) {
-        up[hb] = 1.0f;
+    up = 1.0f;
+    for (int j = 0; j < NJ; ++j)
+        for (int s = 0; s < QS; ++s) qv[j][s] = (qcol && (!F32 || hl == 0)) ? qv[j][s] * p.qscale : 0.0f;
+    if constexpr (F32) {
+        for (int j = 0; j < NJ; ++j) aq32[j] = qv[j][0];
+    } else {
+        float amax = 0.0f;
+        bool finite = true;
         for (int j = 0; j < NJ; ++j)
-            for (int s = 0; s < QS; ++s) qv[hb][j][s] = (qcol[hb] && (!F32 || hl == 0)) ? qv[hb][j][s] * p.qscale : 0.0f;
-        if constexpr (F32) {
-            for (int j = 0; j < NJ; ++j) aq32[j] = qv[hb][j][0];
+            for (int s = 0; s < 8; ++s) {
+                const float a = fabsf(qv[j][s]);
+                amax = fmaxf(amax, a);
+                finite = finite && a <= 3.402823466e38f;
+            }
+        // fp16: one scale for the wave's 8 heads (COLH: for each 8 of its 16, columns 0-7 and 8-15,
+        // as two 8-head waves would take), floating point keeping each element's relative precision.
+        // int8: one per head, over the lanes holding it (columns 2h, 2h + 1 or, COLH, column h; all
+        // q4): the digits are fixed point, so a head with a small q next to a large one keeps its own
+        // precision.
+        if constexpr (KIND == KV_I8) {
+            if (!finite) amax = __builtin_inff();  // (the max carries it to the head's other lanes)
+            amax = max_x16_x32(amax);
+            if constexpr (!COLH) amax = fmaxf(amax, dpp<kQuadSwap1>(amax));
+        } else if constexpr (COLH) {
+            for (int x = 1; x < 8; x <<= 1) amax = fmaxf(amax, __shfl_xor(amax, x));
+            amax = max_x16_x32(amax);
         } else {
-            float amax = 0.0f;
-            bool finite = true;
+            amax = wave_max(amax);
+        }
+        int e = 0;
+        if (amax > 0.0f && amax <= 3.402823466e38f) {
+            frexpf(amax, &e);  // amax < 2^e
+            // fp16: the scaled q stays below 2^14, far from overflow; int8: below 2^7, a digit's range
+            e -= KIND == KV_I8 ? 7 : 14;
+        }
+        float down = ldexpf(1.0f, -e);
+        up = ldexpf(1.0f, e);
+        if (KIND == KV_I8 && !(amax <= 3.402823466e38f)) {
+            // a NaN or infinite q element: the head's scores are NaN, as in floating point (the
+            // digits alone would clamp it to a finite value)
+            down = 0.0f;
+            up = __builtin_nanf("");
+        }
+        if constexpr (KIND == KV_F16) {
             for (int j = 0; j < NJ; ++j)
                 for (int s = 0; s < 8; ++s) {
-                    const float a = fabsf(qv[hb][j][s]);
-                    amax = fmaxf(amax, a);
-                    finite = finite && a <= 3.402823466e38f;
-                }
-            // fp16: one scale for the wave (floating point keeps each element's relative precision).
-            // int8: one per head, over the 8 lanes holding it (columns 2h, 2h + 1, all q4): the digits
-            // are fixed point, so a head with a small q next to a large one keeps its own precision.
-            if constexpr (KIND == KV_I8) {
-                if (!finite) amax = __builtin_inff();  // (the max carries it to the head's other lanes)
-                amax = max_x16_x32(amax);
-                amax = fmaxf(amax, dpp<kQuadSwap1>(amax));
-            } else {
-                amax = wave_max(amax);
-            }
-            int e = 0;
-            if (amax > 0.0f && amax <= 3.402823466e38f) {
-                frexpf(amax, &e);  // amax < 2^e
-                // fp16: the scaled q stays below 2^14, far from overflow; int8: below 2^7, a digit's range
-                e -= KIND == KV_I8 ? 7 : 14;
-            }
-            float down = ldexpf(1.0f, -e);
-            up[hb] = ldexpf(1.0f, e);
-            if (KIND == KV_I8 && !(amax <= 3.402823466e38f)) {
-                // a NaN or infinite q element: the head's scores are NaN, as in floating point (the
-                // digits alone would clamp it to a finite value)
-                down = 0.0f;
-                up[hb] = __builtin_nanf("");
-            }
-            if constexpr (KIND == KV_F16) {
-                for (int j = 0; j < NJ; ++j)
-                    for (int s = 0; s < 8; ++s) {
-                        const float x = qv[hb][j][s] * down;
-                        const _Float16 hi = (_Float16)x;
-                        const _Float16 lo = (_Float16)(x - (float)hi);
-                        aq16[hb][j][s] = hl ? lo : hi;
+                    const float x = qv[j][s] * down;
+                    const _Float16 hi = (_Float16)x;
+                    const _Float16 lo = (_Float16)(x - (float)hi);
+                    if constexpr (COLH) {
+                        aq16[0][j][s] = hi;
+                        aq16[NA - 1][j][s] = lo;
+                    } else {
+                        aq16[0][j][s] = hl ? lo : hi;
                     }
-            } else {
-                // int8 scores run on the integer MFMA, K as stored: x = q * down = d0 + d1 / 2^7 +
-                // d2 / 2^14 + err, |err| <= 2^-15, each digit a signed byte (every step is exact in
-                // fp32). Column 2h (hl == 0) carries d0 into the first MFMA and d2 into the second;
-                // column 2h + 1 carries d1 and zeros. Slot t of load m is d = 64 m + 16 q4 + t, as K's.
-                for (int m = 0; m < T::KLOADS; ++m) {
-                    uint32_t wa[4] = {0u, 0u, 0u, 0u}, wb[4] = {0u, 0u, 0u, 0u};
-                    for (int t = 0; t < 16; ++t) {
-                        const float x = qv[hb][2 * m + (t >> 3)][t & 7] * down;
-                        const float d0 = fminf(fmaxf(__builtin_rintf(x), -127.0f), 127.0f);
-                        const float r1 = (x - d0) * 128.0f;
-                        const float d1 = fminf(fmaxf(__builtin_rintf(r1), -127.0f), 127.0f);
-                        const float d2 = fminf(fmaxf(__builtin_rintf((r1 - d1) * 128.0f), -127.0f), 127.0f);
-                        wa[t >> 2] |= (uint32_t)(uint8_t)(int8_t)(int)(hl ? d1 : d0) << (8 * (t & 3));
-                        wb[t >> 2] |= (hl ? 0u : (uint32_t)(uint8_t)(int8_t)(int)d2) << (8 * (t & 3));
-                    }
-                    aq8[hb][m] = i32x4_t{(int)wa[0], (int)wa[1], (int)wa[2], (int)wa[3]};
-                    aq8[hb][T::KLOADS + m] = i32x4_t{(int)wb[0], (int)wb[1], (int)wb[2], (int)wb[3]};
                 }
+        } else {
+            // int8 scores run on the integer MFMA, K as stored: x = q * down = d0 + d1 / 2^7 +
+            // d2 / 2^14 + err, |err| <= 2^-15, each digit a signed byte (every step is exact in
+            // fp32). Column 2h (hl == 0) carries d0 into the first MFMA and d2 into the second;
+            // column 2h + 1 carries d1 and zeros. COLH: column h carries d0, d1 and d2 into three.
+            // Slot t of load m is d = 64 m + 16 q4 + t, as K's.
+            for (int m = 0; m < T::KLOADS; ++m) {
+                uint32_t wa[4] = {0u, 0u, 0u, 0u}, wb[4] = {0u, 0u, 0u, 0u}, wc[4] = {0u, 0u, 0u, 0u};
+                for (int t = 0; t < 16; ++t) {
+                    const float x = qv[2 * m + (t >> 3)][t & 7] * down;
+                    const float d0 = fminf(fmaxf(__builtin_rintf(x), -127.0f), 127.0f);
+                    const float r1 = (x - d0) * 128.0f;
+                    const float d1 = fminf(fmaxf(__builtin_rintf(r1), -127.0f), 127.0f);
+                    const float d2 = fminf(fmaxf(__builtin_rintf((r1 - d1) * 128.0f), -127.0f), 127.0f);
+                    auto byte = [&](float d) { return (uint32_t)(uint8_t)(int8_t)(int)d << (8 * (t & 3)); };
+                    if constexpr (COLH) {
+                        wa[t >> 2] |= byte(d0);
+                        wb[t >> 2] |= byte(d1);
+                        wc[t >> 2] |= byte(d2);
+                    } else {
+                        wa[t >> 2] |= byte(hl ? d1 : d0);
+                        wb[t >> 2] |= hl ? 0u : byte(d2);
+                    }
+                }
+                aq8[m] = i32x4_t{(int)wa[0], (int)wa[1], (int)wa[2], (int)wa[3]};
+                aq8[T::KLOADS + m] = i32x4_t{(int)wb[0], (int)wb[1], (int)wb[2], (int)wb[3]};
+                if constexpr (COLH) aq8[2 * T::KLOADS + m] = i32x4_t{(int)wc[0], (int)wc[1], (int)wc[2], (int)wc[3]};
             }
         }
     }
@@ -722,16 +754,14 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
             }
     };
 
-    // ---- per-wave online-softmax state. Lane (c, q4) holds column c (head c/2) for the tokens
-    // 16h + 4*q4 + i of each tile (slot j = 4h + i of the P^T operand): m is uniform over the 8
-    // lanes of a head, l is the lane's partial sum over its tokens.
-    float m[HB], l[HB];
-    floatx4_t acc[HB][NMB];
-    for (int hb = 0; hb < HB; ++hb) {
-        m[hb] = kNegBig;
-        l[hb] = 0.0f;
-        for (int mb = 0; mb < NMB; ++mb) acc[hb][mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    }
+    // ---- per-wave online-softmax state. Lane (c, q4) holds column c (head hh) for the tokens
+    // 16h + 4*q4 + i of each tile (slot j = 4h + i of the P^T operand): m is uniform over the lanes
+    // of a head, l is the lane's partial sum over its tokens. acc[a][mb]: O^T rows 16 mb.., set a
+    // (COLH: the high parts' products, then the low parts'; else both, in columns 2h and 2h + 1).
+    float m = kNegBig, l = 0.0f;
+    floatx4_t acc[NA][NMB];
+    for (int a = 0; a < NA; ++a)
+        for (int mb = 0; mb < NMB; ++mb) acc[a][mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     uint32_t lsink = 0;  // LOADS: what the tiles' registers XOR to
     auto compute_tile = [&](const R& r, int tt) {
@@ -747,32 +777,42 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
             return;
         }
         store_v(r);
-        // S^T = K Q^T for both halves
-        floatx4_t S[HB][2];
-        for (int h = 0; h < 2; ++h)
-            for (int hb = 0; hb < HB; ++hb) {
-                S[hb][h] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                if constexpr (F32) {
-                    for (int j = 0; j < NJ; ++j) {
-                        const uint4 w4 = r.k[h][j >> 2];
-                        const uint32_t w = (j & 3) == 0 ? w4.x : (j & 3) == 1 ? w4.y : (j & 3) == 2 ? w4.z : w4.w;
-                        S[hb][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, w), aq32[j], S[hb][h], 0, 0, 0);
-                    }
-                } else if constexpr (KIND == KV_F16) {
+        // S^T = K Q^T for both halves. S[a][h]: a = 0 the column's part (COLH: the high part,
+        // int8 d0 + d2 / 2^14), a = 1 (COLH) the low part (int8 d1 / 2^7): the values columns 2h and
+        // 2h + 1 hold in the two-column layout.
+        floatx4_t S[NA][2];
+        for (int h = 0; h < 2; ++h) {
+            for (int a = 0; a < NA; ++a) S[a][h] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (F32) {
+                for (int j = 0; j < NJ; ++j) {
+                    const uint4 w4 = r.k[h][j >> 2];
+                    const uint32_t w = (j & 3) == 0 ? w4.x : (j & 3) == 1 ? w4.y : (j & 3) == 2 ? w4.z : w4.w;
+                    S[0][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, w), aq32[j], S[0][h], 0, 0, 0);
+                }
+            } else if constexpr (KIND == KV_F16) {
+                for (int a = 0; a < NA; ++a)
                     for (int j = 0; j < NJ; ++j)
-                        S[hb][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, r.k[h][j]), aq16[hb][j], S[hb][h], 0, 0, 0);
-                } else {
-                    // exact integer dot products per digit; the two scaled sums are the column's part
-                    i32x4_t SA = {0, 0, 0, 0}, SB = {0, 0, 0, 0};
-                    for (int m = 0; m < T::KLOADS; ++m) {
-                        const i32x4_t kk = __builtin_bit_cast(i32x4_t, r.k[h][m]);
-                        SA = __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, aq8[hb][m], SA, 0, 0, 0);
-                        SB = __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, aq8[hb][T::KLOADS + m], SB, 0, 0, 0);
+                        S[a][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, r.k[h][j]), aq16[a][j], S[a][h], 0, 0, 0);
+            } else {
+                // exact integer dot products per digit; the scaled sums are the column's part
+                i32x4_t SA = {0, 0, 0, 0}, SB = {0, 0, 0, 0}, SC = {0, 0, 0, 0};
+                for (int m = 0; m < T::KLOADS; ++m) {
+                    const i32x4_t kk = __builtin_bit_cast(i32x4_t, r.k[h][m]);
+                    SA = __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, aq8[m], SA, 0, 0, 0);
+                    SB = __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, aq8[T::KLOADS + m], SB, 0, 0, 0);
+                    if constexpr (COLH) SC = __builtin_amdgcn_mfma_i32_16x16x64_i8(kk, aq8[2 * T::KLOADS + m], SC, 0, 0, 0);
+                }
+                if constexpr (COLH) {
+                    for (int i = 0; i < 4; ++i) {
+                        S[0][h][i] = __builtin_fmaf((float)SC[i], 1.0f / 16384.0f, (float)SA[i] * 1.0f);
+                        S[NA - 1][h][i] = (float)SB[i] * (1.0f / 128.0f);  // (exact: a power of two)
                     }
+                } else {
                     const float wa = hl ? 1.0f / 128.0f : 1.0f, wb = hl ? 0.0f : 1.0f / 16384.0f;
-                    for (int i = 0; i < 4; ++i) S[hb][h][i] = __builtin_fmaf((float)SB[i], wb, (float)SA[i] * wa);
+                    for (int i = 0; i < 4; ++i) S[0][h][i] = __builtin_fmaf((float)SB[i], wb, (float)SA[i] * wa);
                 }
             }
+        }
         // int8, FAST: the scales of the two halves (the first's for both with tile_in_page), from the
         // lanes that hold them when the partition's scales are in lanes
         float ksh[2], vsh[2];
@@ -797,23 +837,25 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
             if (vmx > 0.0f) frexpf(vmx, &e);  // vmx < 2^e
             if (e > ve) {  // wave-uniform
                 const float down = ldexpf(1.0f, ve - e);
-                for (int hb = 0; hb < HB; ++hb)
-                    for (int mb = 0; mb < NMB; ++mb) acc[hb][mb] *= down;
+                for (int a = 0; a < NA; ++a)
+                    for (int mb = 0; mb < NMB; ++mb) acc[a][mb] *= down;
                 ve = e;
                 vdown = ldexpf(1.0f, -e);
             }
         }
-        // scores of this lane's 8 tokens for head c/2: high + low columns, scaled, masked
-        half8_t pb16[HB];
+        // scores of this lane's 8 tokens for head hh: high + low columns (COLH: parts), scaled,
+        // masked. pb16[a]: the P^T operand of the P*V MFMAs (COLH: p's high parts, then low parts).
+        half8_t pb16[NA];
         float pb32[F32 ? 8 : 1];
-        for (int hb = 0; hb < HB; ++hb) {
+        {
             float s[8];
             for (int h = 0; h < 2; ++h)
                 for (int i = 0; i < 4; ++i) {
                     const int j = 4 * h + i;
-                    float f = up[hb];
+                    float f = up;
                     if constexpr (KIND == KV_I8) f *= FAST ? ksh[h] : r.ks[j];
-                    s[j] = (S[hb][h][i] + dpp<kQuadSwap1>(S[hb][h][i])) * f;
+                    if constexpr (COLH) s[j] = (S[0][h][i] + S[NA - 1][h][i]) * f;
+                    else s[j] = (S[0][h][i] + dpp<kQuadSwap1>(S[0][h][i])) * f;
                 }
             // Tokens past the partition end score kNegBig; only a partition's last tile has any, so the
             // compare-and-select runs under a wave-uniform branch. (p = exp2(kNegBig - m) below is then
@@ -824,27 +866,37 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
             float mx = kNegBig;
             for (int j = 0; j < 8; ++j) mx = fmaxf(mx, s[j]);
             mx = max_x16_x32(mx);
-            const float mn = fmaxf(m[hb], mx);
-            const float corr = __builtin_amdgcn_exp2f(m[hb] - mn);
-            m[hb] = mn;
+            const float mn = fmaxf(m, mx);
+            const float corr = __builtin_amdgcn_exp2f(m - mn);
+            m = mn;
             float psum = 0.0f;
             for (int j = 0; j < 8; ++j) {
                 const float pr = __builtin_amdgcn_exp2f(s[j] - mn);
                 psum += pr;
                 float pv = pr;
-                if constexpr (KIND == KV_I8) pv *= (FAST ? vsh[j >> 2] : r.vs[j]) * vdown;
+                const float xs = KIND == KV_I8 ? (FAST ? vsh[j >> 2] : r.vs[j]) * vdown : 1.0f;
+                if constexpr (KIND == KV_I8) pv *= xs;
                 if constexpr (F32) {
                     pb32[j] = hl ? 0.0f : pv;
                 } else {
-                    const _Float16 hi = (_Float16)pv;
-                    pb16[hb][j] = hl ? (_Float16)(pv - (float)hi) : hi;
+                    if constexpr (COLH) {
+                        // (the low part as p * xs - hi from the exact product, the form the 8-head
+                        // build takes)
+                        const _Float16 hi = pinned((_Float16)pv);
+                        pb16[0][j] = hi;
+                        pb16[NA - 1][j] = (_Float16)__builtin_fmaf(pr, xs, -(float)hi);
+                    } else {
+                        const _Float16 hi = (_Float16)pv;
+                        pb16[0][j] = hl ? (_Float16)(pv - (float)hi) : hi;
+                    }
                 }
             }
-            l[hb] = l[hb] * corr + psum;
+            l = l * corr + psum;
             // corr is 1 for every head whose running max did not grow: skip the no-op rescale (the
             // accumulators may live in AGPRs, where a multiply costs two moves as well)
             if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0)
-                for (int mb = 0; mb < NMB; ++mb) acc[hb][mb] *= corr;
+                for (int a = 0; a < NA; ++a)
+                    for (int mb = 0; mb < NMB; ++mb) acc[a][mb] *= corr;
         }
         // LDS ops of one wave execute in order; the fence keeps the compiler from moving the V^T
         // reads above the stores.
@@ -857,8 +909,8 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
             if constexpr (F32) {
                 for (int u = 0; u < 8; ++u) {
                     const int t = 16 * (u >> 2) + 4 * q4 + (u & 3);
-                    const float a = *reinterpret_cast<const float*>(vt + t * D * 4 + 16 * ((d >> 2) ^ T::swz(t)) + 4 * (d & 3));
-                    acc[0][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, pb32[u], acc[0][mb], 0, 0, 0);
+                    const float va = *reinterpret_cast<const float*>(vt + t * D * 4 + 16 * ((d >> 2) ^ T::swz(t)) + 4 * (d & 3));
+                    acc[0][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, pb32[u], acc[0][mb], 0, 0, 0);
                 }
             } else if constexpr (KIND == KV_F16) {
                 // two reads: tokens 4 q4 + k, then 16 + 4 q4 + k (k < 4), of column d
@@ -867,17 +919,17 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
                     (lds_fp16x4_t*)(vt + t0 * D * 2 + 16 * (ch ^ T::vswz(t0)) + off));
                 const fp16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
                     (lds_fp16x4_t*)(vt + t1 * D * 2 + 16 * (ch ^ T::vswz(t1)) + off));
-                const half8_t a = __builtin_bit_cast(half8_t, (fp16x8_t){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-                for (int hb = 0; hb < HB; ++hb)
-                    acc[hb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb16[hb], acc[hb][mb], 0, 0, 0);
+                const half8_t va = __builtin_bit_cast(half8_t, (fp16x8_t){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+                for (int a = 0; a < NA; ++a)
+                    acc[a][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb16[a], acc[a][mb], 0, 0, 0);
             } else {
                 // one read: the 8 tokens of column d as bytes, widened to exact fp16
                 const int k = c >> 1, t = (k < 4 ? 0 : 12) + 4 * q4 + k;
                 const i32x2_t x = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
                     (lds_i32x2_t*)(vt + t * D + 16 * (mb ^ T::vswz(t)) + 8 * (c & 1)));
-                const half8_t a = i8x8_to_half8(x[0], x[1]);
-                for (int hb = 0; hb < HB; ++hb)
-                    acc[hb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb16[hb], acc[hb][mb], 0, 0, 0);
+                const half8_t va = i8x8_to_half8(x[0], x[1]);
+                for (int a = 0; a < NA; ++a)
+                    acc[a][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb16[a], acc[a][mb], 0, 0, 0);
             }
         }
         // the next store_v overwrites the tile: keep it after these reads
@@ -898,30 +950,36 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
     // score (p = 0, corr = 1 exactly), reads zeros or masked rows, and at most renormalises the
     // int8 accumulators by a power of two, so it changes nothing. (sched_barrier: the scheduler
     // would otherwise move part of the prefetch across the wait or below the computation.)
-    // ---- the wave's state -> LDS: [8 HB][D] fp32 and (m, l). The lanes of column pair (2 hh, 2 hh + 1)
+    // ---- the wave's state -> LDS: [HQ][D] fp32 and (m, l). The lanes of column pair (2 hh, 2 hh + 1)
     // hold the high and low parts of d = 16 mb + 4 q4 + i (i < 4) of head hh; their sums form one
     // 16-byte chunk per mb, of which lane hl writes values 2 hl and 2 hl + 1 (no lane idles and no
-    // branch splits the swaps from the adds). Chunk c of head h's row is stored at c ^ (h & 7) so that
-    // the 8 heads' rows do not all start in the same LDS banks. Heads past qg (PART, or QG 4 and less)
-    // are written too and never read. `live`: false writes an empty state (a wave with no tile in
-    // that partition).
+    // branch splits the swaps from the adds). COLH: lane (hh, q4) holds both parts of its head's
+    // chunk and writes it whole. Chunk c of head h's row is stored at c ^ (h & 7) so that the 8
+    // heads' rows do not all start in the same LDS banks. Heads past qg (PART, or QG 4 and less) are
+    // written too and never read. `live`: false writes an empty state (a wave with no tile in that
+    // partition).
     auto state_to_lds = [&](float* dst, float2* dml, bool live) {
         const float vupf = KIND == KV_I8 ? ldexpf(1.0f, ve) : 1.0f;
-        for (int hb = 0; hb < HB; ++hb) {
-            const int hq = 8 * hb + hh;  // the workgroup's head of this lane's column
-            const float lsum = sum_x16_x32(l[hb]);
-            for (int mb = 0; mb < NMB; ++mb) {
+        const float lsum = sum_x16_x32(l);
+        for (int mb = 0; mb < NMB; ++mb) {
+            float* chunk = dst + hh * D + 4 * ((4 * mb + q4) ^ (hh & 7));
+            if constexpr (COLH) {
+                const floatx4_t a = acc[0][mb], z = acc[NA - 1][mb];
+                float4 v = make_float4(a[0] + z[0], a[1] + z[1], a[2] + z[2], a[3] + z[3]);
+                v = live ? make_float4(v.x * vupf, v.y * vupf, v.z * vupf, v.w * vupf) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                *reinterpret_cast<float4*>(chunk) = v;
+            } else {
                 // lane hl keeps values 2 hl, 2 hl + 1 and sends the other two, which its partner
                 // (lane l ^ 1, the other part) keeps
-                const floatx4_t a = acc[hb][mb];
+                const floatx4_t a = acc[0][mb];
                 const float k0 = hl ? a[2] : a[0], k1 = hl ? a[3] : a[1];
                 const float x0 = hl ? a[0] : a[2], x1 = hl ? a[1] : a[3];
                 float2 v = make_float2(k0 + quad_swap1(x0), k1 + quad_swap1(x1));
                 v = live ? make_float2(v.x * vupf, v.y * vupf) : make_float2(0.0f, 0.0f);
-                *reinterpret_cast<float2*>(dst + hq * D + 4 * ((4 * mb + q4) ^ (hq & 7)) + 2 * hl) = v;
+                *reinterpret_cast<float2*>(chunk + 2 * hl) = v;
             }
-            if (hl == 0 && qcol[hb] && q4 == 0) dml[hq] = live ? make_float2(m[hb], lsum) : make_float2(kNegBig, 0.0f);
         }
+        if (hl == 0 && qcol && q4 == 0) dml[hh] = live ? make_float2(m, lsum) : make_float2(kNegBig, 0.0f);
     };
 
     // PAIR: `cur` is the partition of the range (0 or 1) the wave's state belongs to. At its first
@@ -939,11 +997,10 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
             if constexpr (PAIR && !LOADS) {
                 if (cur == 0 && it >= tpp && it < ntiles) {  // wave-uniform
                     state_to_lds(s_part[wave], s_ml2[wave], true);
-                    for (int hb = 0; hb < HB; ++hb) {
-                        m[hb] = kNegBig;
-                        l[hb] = 0.0f;
-                        for (int mb = 0; mb < NMB; ++mb) acc[hb][mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                    }
+                    m = kNegBig;
+                    l = 0.0f;
+                    for (int a = 0; a < NA; ++a)
+                        for (int mb = 0; mb < NMB; ++mb) acc[a][mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
                     ve = -160;
                     vdown = 1.0f;
                     cur = 1;

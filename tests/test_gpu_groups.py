@@ -134,11 +134,14 @@ def test_groups_workspace_slots(gpu, oracle, shape, qg, kv):
 @pytest.mark.parametrize("lens,part", [([1000, 1000], 256), ([1000, 1000], 128), ([777, 65, 300, 1], 128),
                                        ([4096, 4096, 4096, 4096], 512), ([500, 300, 120], 160)])
 def test_sibling_workgroups_give_group8_bits(gpu, kv, lens, part):
-    """Group 16: f16 runs one workgroup of two 8-head blocks per KV head, i8 one workgroup of two
-    head splits (each split's four waves walk the tiles as a group-8 workgroup's), f32 two workgroups
-    of 8 (with the sibling order when the (KV head, sequence, partition) units fill blocks of 8, else
-    without it). Each block of 8 heads gives the same bits as a group-8 run over the same K/V with
-    those heads as the group."""
+    """Group 16: f16 and i8 run one workgroup of 16-head waves per KV head (one head per score
+    column, the high and low parts in separate MFMAs), f32 two workgroups of 8 (with the sibling
+    order when the (KV head, sequence, partition) units fill blocks of 8, else without it). Each 8
+    of the 16 heads give the same result as a group-8 run over the same K/V with those heads as the
+    group: bit for bit for f16 and f32; for i8 within the fp32 rounding of p * v_scale's split into
+    fp16 parts, which the compiler forms from the exact or the rounded product per build (1e-7 of
+    max |v|; a high part the MFMA received that differed from the one its low part was taken
+    against once showed here as 2.3e-6)."""
     kvb = gpu
     B = len(lens)
     w16 = kvb.Workload(kvb.Shape(B, 32, 2, 128), kv, lens, seed=len(lens) * 31 + part)
@@ -161,8 +164,12 @@ def test_sibling_workgroups_give_group8_bits(gpu, kv, lens, part):
         d8.run(part)
         out8 = d8.output()
         d8.free()
-        assert np.array_equal(out16[:, heads].view(np.uint32), out8.view(np.uint32)), half
-    progress(f"[groups] group 16 = 2 x group 8 bits, {kv} lens {lens} part {part} ({units} units)")
+        if kv == "i8":
+            vmax = float(np.abs(c16.dequantized(w16)[1]).max())
+            assert np.abs(out16[:, heads] - out8).max() <= 1e-7 * vmax, half
+        else:
+            assert np.array_equal(out16[:, heads].view(np.uint32), out8.view(np.uint32)), half
+    progress(f"[groups] group 16 = 2 x group 8, {kv} lens {lens} part {part} ({units} units)")
 
 
 @pytest.mark.parametrize("kv", ["f16", "i8"])
