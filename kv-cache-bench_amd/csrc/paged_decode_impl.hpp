@@ -367,6 +367,13 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
     constexpr bool COLH = QW == 16;
     constexpr int NA = COLH ? 2 : 1;      // accumulator sets: one, or (COLH) high and low
     constexpr int HQ = COLH ? 16 : 8;     // rows of a wave's state in LDS (heads, the ones past qg unread)
+    // Lazy rescaling (16-head waves): the running max m is a reference that moves only when a tile's
+    // max passes it by more than kLazyRescale (p <= 2^8, in range for the fp16 parts), and the true
+    // max mt is kept beside it for the partition's stored state. A 16-head wave's accumulators live
+    // in AGPRs, where a rescale costs a read, a multiply and a write per value, and with 16 heads some
+    // head's max grows on most tiles (about 27 of a c4 wave's 32). 8-head waves rescale eagerly.
+    constexpr bool LAZY = COLH;
+    constexpr float kLazyRescale = 8.0f;
     // Tile register buffers per wave: one computed while the next is loaded (see the tile walk).
     // fp32 tiles are too large for more than one. (Three for int8, whose tiles are half an fp16
     // tile, spill at head_dim 128 and measured slower.)
@@ -384,11 +391,13 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
     constexpr int SVB = kTok * T::LDS_ESZ >= HQ * 4 ? kTok * D * T::LDS_ESZ : HQ * D * 4;
     __shared__ __attribute__((aligned(16))) unsigned char s_v[W][SVB];
     __shared__ float2 s_ml[W][QW];
+    __shared__ float s_mt[LAZY ? W : 1][QW];  // LAZY: each wave's true max per head
     // PAIR: each wave's state for the first partition, [QG][D] fp32 and (m, l), as the V tile holds
     // the last partition's after the walk (room for 8 heads at least: state_to_lds writes all 8 of a
     // head block, the heads past qg unread)
     __shared__ __attribute__((aligned(16))) float s_part[PAIR ? W : 1][PAIR ? HQ * D : 4];
     __shared__ float2 s_ml2[PAIR ? W : 1][QW];
+    __shared__ float s_mt2[PAIR && LAZY ? W : 1][QW];
 
     // Grid (H / qg, B, max_parts), head group fastest: workgroups go to the 8 XCDs round robin by
     // linear id, so consecutive ids (one partition of consecutive head groups and sequences) spread
@@ -759,6 +768,7 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
     // of a head, l is the lane's partial sum over its tokens. acc[a][mb]: O^T rows 16 mb.., set a
     // (COLH: the high parts' products, then the low parts'; else both, in columns 2h and 2h + 1).
     float m = kNegBig, l = 0.0f;
+    float mt = kNegBig;  // LAZY: the true running max (m is then the reference the p are taken against)
     floatx4_t acc[NA][NMB];
     for (int a = 0; a < NA; ++a)
         for (int mb = 0; mb < NMB; ++mb) acc[a][mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -866,7 +876,13 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
             float mx = kNegBig;
             for (int j = 0; j < 8; ++j) mx = fmaxf(mx, s[j]);
             mx = max_x16_x32(mx);
-            const float mn = fmaxf(m, mx);
+            float mn;
+            if constexpr (LAZY) {
+                mt = fmaxf(mt, mx);
+                mn = mx > m + kLazyRescale ? mt : m;  // (the first live tile always moves it)
+            } else {
+                mn = fmaxf(m, mx);
+            }
             const float corr = __builtin_amdgcn_exp2f(m - mn);
             m = mn;
             float psum = 0.0f;
@@ -958,7 +974,7 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
     // heads' rows do not all start in the same LDS banks. Heads past qg (PART, or QG 4 and less) are
     // written too and never read. `live`: false writes an empty state (a wave with no tile in that
     // partition).
-    auto state_to_lds = [&](float* dst, float2* dml, bool live) {
+    auto state_to_lds = [&](float* dst, float2* dml, float* dmt, bool live) {
         const float vupf = KIND == KV_I8 ? ldexpf(1.0f, ve) : 1.0f;
         const float lsum = sum_x16_x32(l);
         for (int mb = 0; mb < NMB; ++mb) {
@@ -979,7 +995,10 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
                 *reinterpret_cast<float2*>(chunk + 2 * hl) = v;
             }
         }
-        if (hl == 0 && qcol && q4 == 0) dml[hh] = live ? make_float2(m, lsum) : make_float2(kNegBig, 0.0f);
+        if (hl == 0 && qcol && q4 == 0) {
+            dml[hh] = live ? make_float2(m, lsum) : make_float2(kNegBig, 0.0f);
+            if constexpr (LAZY) dmt[hh] = live ? mt : kNegBig;
+        }
     };
 
     // PAIR: `cur` is the partition of the range (0 or 1) the wave's state belongs to. At its first
@@ -996,8 +1015,9 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (PAIR && !LOADS) {
                 if (cur == 0 && it >= tpp && it < ntiles) {  // wave-uniform
-                    state_to_lds(s_part[wave], s_ml2[wave], true);
+                    state_to_lds(s_part[wave], s_ml2[wave], s_mt2[LAZY ? wave : 0], true);
                     m = kNegBig;
+                    mt = kNegBig;
                     l = 0.0f;
                     for (int a = 0; a < NA; ++a)
                         for (int mb = 0; mb < NMB; ++mb) acc[a][mb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1035,11 +1055,11 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
     bool last_live = true;
     if constexpr (PAIR) {
         if (ng == 2 && cur == 0) {  // wave-uniform
-            state_to_lds(s_part[wave], s_ml2[wave], true);
+            state_to_lds(s_part[wave], s_ml2[wave], s_mt2[LAZY ? wave : 0], true);
             last_live = false;
         }
     }
-    state_to_lds(sacc, s_ml[wave], last_live);
+    state_to_lds(sacc, s_ml[wave], s_mt[LAZY ? wave : 0], last_live);
     __syncthreads();
 #ifdef KVB_WG_TIMESTAMPS
     unsigned long long ts_slowest = 0;
@@ -1069,6 +1089,13 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
         };
         float M = kNegBig;
         for (int w = 0; w < TS; ++w) M = fmaxf(M, wml(w).x);
+        // LAZY: the waves' states are taken against their reference maxes; the partition's stored
+        // (m, l) against the true one, Mt >= M (its o, a ratio, is the same either way)
+        float Mt = M;
+        if constexpr (LAZY) {
+            Mt = kNegBig;
+            for (int w = 0; w < TS; ++w) Mt = fmaxf(Mt, lastp ? s_mt[w0 + w][lh] : s_mt2[PAIR ? w : 0][lh]);
+        }
         float L = 0.0f;
         float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         for (int w = 0; w < TS; ++w) {
@@ -1090,7 +1117,8 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
         if (ed == 0) {  // (m, l) as one 8-byte agent-scope store
             const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(
                 p.part_ml + slot0, (short)0, NQ * p.max_parts * 8, 0x00020000);
-            const u32x2_t ml = {__builtin_bit_cast(uint32_t, M * kLn2), __builtin_bit_cast(uint32_t, L)};
+            const float Ls = LAZY ? L * __builtin_amdgcn_exp2f(M - Mt) : L;
+            const u32x2_t ml = {__builtin_bit_cast(uint32_t, Mt * kLn2), __builtin_bit_cast(uint32_t, Ls)};
             __builtin_amdgcn_raw_buffer_store_b64(ml, rml, eh * p.max_parts * 8, 0, kScopeAgent);
         }
         if (p.out && len <= p.part_tokens)  // one partition: this is the output

@@ -148,14 +148,30 @@ MUTANTS = [
       "const float w = ml[2 * i + 1] * exp_ftz(ml[2 * i] - M);", "const float w = exp_ftz(ml[2 * i] - M);"),
     # ---- the shipped kernels' source, run on the CPU emulation (reference: scripts/mutation.sh:50-59) ----
     X("online-softmax rescale dropped (corr = 1)",
-      "const float corr = __builtin_amdgcn_exp2f(m[hb] - mn);", "const float corr = 1.0f;"),
-    X("softmax scale not applied", "qv[hb][j][s] * p.qscale : 0.0f;", "qv[hb][j][s] : 0.0f;"),
-    X("q loaded for the head block's first head in every column",
-      "h0 + (qcol[hb] ? 8 * hb + hh : 0)) * D;", "h0 + (qcol[hb] ? 8 * hb : 0)) * D;"),
+      "const float corr = __builtin_amdgcn_exp2f(m - mn);", "const float corr = 1.0f;"),
+    X("softmax scale not applied", "qv[j][s] * p.qscale : 0.0f;", "qv[j][s] : 0.0f;"),
+    X("q loaded for the wave's first head in every column",
+      "hw0 + (qcol ? hh : 0)) * D;", "hw0 + (qcol ? 0 : 0)) * D;"),
+    X("head splits: every split serves the workgroup's first heads",
+      "const int hw0 = HS == 1 ? h0 : h0 + (wave / TS) * QW;", "const int hw0 = h0;"),
+    X("head splits: the wave merge takes the first split's waves for every head",
+      "const int w0 = HS == 1 ? 0 : (eh / QW) * TS,", "const int w0 = 0,"),
     X("fp16 q: low column dropped (q as one fp16 number)",
-      "aq16[hb][j][s] = hl ? lo : hi;", "aq16[hb][j][s] = hl ? (_Float16)0.0f : hi;"),
+      "aq16[0][j][s] = hl ? lo : hi;", "aq16[0][j][s] = hl ? (_Float16)0.0f : hi;"),
+    X("fp16 q, 16-head waves: low parts dropped",
+      "aq16[NA - 1][j][s] = lo;", "aq16[NA - 1][j][s] = (_Float16)0.0f;"),
+    X("fp16 q, 16-head waves: one scale for all 16 heads (not one per 8)",
+      "for (int x = 1; x < 8; x <<= 1) amax = fmaxf(amax, __shfl_xor(amax, x));",
+      "for (int x = 1; x < 16; x <<= 1) amax = fmaxf(amax, __shfl_xor(amax, x));"),
     X("scores: the low column's DPP sum dropped",
-      "s[j] = (S[hb][h][i] + dpp<kQuadSwap1>(S[hb][h][i])) * f;", "s[j] = S[hb][h][i] * f;"),
+      "else s[j] = (S[0][h][i] + dpp<kQuadSwap1>(S[0][h][i])) * f;", "else s[j] = S[0][h][i] * f;"),
+    X("scores, 16-head waves: the low part's MFMA dropped",
+      "if constexpr (COLH) s[j] = (S[0][h][i] + S[NA - 1][h][i]) * f;", "if constexpr (COLH) s[j] = S[0][h][i] * f;"),
+    X("int8 q, 16-head waves: second digit weighted 2^-6 instead of 2^-7",
+      "S[NA - 1][h][i] = (float)SB[i] * (1.0f / 128.0f);", "S[NA - 1][h][i] = (float)SB[i] * (1.0f / 64.0f);"),
+    X("int8 q, 16-head waves: third digit dropped",
+      "S[0][h][i] = __builtin_fmaf((float)SC[i], 1.0f / 16384.0f, (float)SA[i] * 1.0f);",
+      "S[0][h][i] = (float)SA[i];"),
     X("int8 q: second digit weighted 2^-6 instead of 2^-7",
       "const float wa = hl ? 1.0f / 128.0f : 1.0f,", "const float wa = hl ? 1.0f / 64.0f : 1.0f,"),
     X("int8 q: third digit dropped", "wb = hl ? 0.0f : 1.0f / 16384.0f;", "wb = 0.0f;"),
@@ -164,9 +180,14 @@ MUTANTS = [
       "const int soff = lane < nb ? (max(blkv, 0) * Hkv + kvh) * 4 : 0;",
       "const int soff = lane < nb ? (max(blkv, 0) * Hkv) * 4 : 0;"),
     X("p: low fp16 column dropped (p as one fp16 number)",
-      "pb16[hb][j] = hl ? (_Float16)(pv - (float)hi) : hi;", "pb16[hb][j] = hl ? (_Float16)0.0f : hi;"),
+      "pb16[0][j] = hl ? (_Float16)(pv - (float)hi) : hi;", "pb16[0][j] = hl ? (_Float16)0.0f : hi;"),
+    X("p, 16-head waves: low parts dropped",
+      "pb16[NA - 1][j] = (_Float16)__builtin_fmaf(pr, xs, -(float)hi);", "pb16[NA - 1][j] = (_Float16)0.0f;"),
+    X("P*V, 16-head waves: the low parts' accumulators left out of the wave's state",
+      "float4 v = make_float4(a[0] + z[0], a[1] + z[1], a[2] + z[2], a[3] + z[3]);",
+      "float4 v = make_float4(a[0], a[1], a[2], a[3]);"),
     X("int8: p * v_scale not normalised by the running power of two",
-      "pv *= (FAST ? vsh[j >> 2] : r.vs[j]) * vdown;", "pv *= FAST ? vsh[j >> 2] : r.vs[j];"),
+      "(FAST ? vsh[j >> 2] : r.vs[j]) * vdown : 1.0f;", "(FAST ? vsh[j >> 2] : r.vs[j]) : 1.0f;"),
     X("int8: the V-scale power of two not undone at the end",
       "const float vupf = KIND == KV_I8 ? ldexpf(1.0f, ve) : 1.0f;", "const float vupf = 1.0f;"),
     X("tail mask off by one (the token at the partition end scored)",
@@ -184,7 +205,7 @@ MUTANTS = [
     X("wave merge weight exp(M - m) instead of exp(m - M)",
       "const float wt = __builtin_amdgcn_exp2f(wml(w).x - M);", "const float wt = __builtin_amdgcn_exp2f(M - wml(w).x);"),
     X("wave merge reads the other waves' rows without their swizzle",
-      "wacc(w) + eh * D + 4 * (ed ^ (eh & 7)));", "wacc(w) + eh * D + 4 * ed);"),
+      "wacc(w) + lh * D + 4 * (ed ^ (lh & 7)));", "wacc(w) + lh * D + 4 * ed);"),
     X("partition output not divided by its sum",
       "const float4 r = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);",
       "const float4 r = make_float4(o.x, o.y, o.z, o.w);"),

@@ -244,25 +244,29 @@ def test_c_abi_auto_part_tokens_thresholds(kvb, oracle):
 
 
 def test_heads_per_workgroup(kvb):
-    """kvb_heads_per_workgroup: one workgroup reads each K/V page for this many query heads. 16
-    for a group that is a multiple of 16 with an f16 cache (two blocks of 8 heads), else the
-    largest divisor of the group that is at most 8; 1 without share_kv; -1 for shapes the decode
-    refuses. Spot values, then every group to 64 against a brute-force search."""
+    """kvb_heads_per_workgroup: one workgroup reads each K/V page for this many query heads. 32 or
+    16 for a group that is a multiple of 32 or 16 with an f16 or i8 cache (16-head waves: one
+    workgroup of four, or two head splits), else the largest divisor of the group that is at most 8;
+    1 without share_kv; -1 for shapes the decode refuses. Spot values, then every group to 64
+    against a brute-force search."""
     spot = {1: 1, 2: 2, 3: 3, 4: 4, 5: 5, 6: 6, 7: 7, 8: 8, 9: 3, 10: 5, 11: 1, 12: 6, 13: 1, 14: 7, 15: 5,
-            16: 8, 18: 6, 20: 5, 21: 7, 24: 8, 28: 7, 40: 8, 64: 8}
+            16: 8, 18: 6, 20: 5, 21: 7, 24: 8, 28: 7, 32: 8, 40: 8, 48: 8, 64: 8}
     F32, F16, I8 = kvb.KV_F32, kvb.KV_F16, kvb.KV_I8
+
+    def wide(g, want):  # f16 and i8
+        return 32 if g % 32 == 0 else 16 if g % 16 == 0 else want
+
     for g, want in spot.items():
         assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, F32, 1) == want, g
-        want16 = 16 if g % 16 == 0 else want
-        assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, F16, 1) == want16, g
-        assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, I8, 1) == want, g
+        assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, F16, 1) == wide(g, want), g
+        assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, I8, 1) == wide(g, want), g
         for kv in (F32, F16, I8):
             assert kvb.hip.kvb_heads_per_workgroup(g * 8, 8, kv, 0) == 1
     for g in range(1, 65):
-        for kv in (F32, F16):
+        for kv in (F32, F16, I8):
             got = kvb.hip.kvb_heads_per_workgroup(g * 2, 2, kv, 1)
-            if kv == F16 and g % 16 == 0:
-                assert got == 16
+            if kv != F32 and g % 16 == 0:
+                assert got == (32 if g % 32 == 0 else 16), g
                 continue
             assert g % got == 0 and got <= 8
             assert all(g % d != 0 for d in range(got + 1, 9)), g
@@ -271,8 +275,9 @@ def test_heads_per_workgroup(kvb):
     assert kvb.hip.kvb_heads_per_workgroup(16, 8, 3, 1) == -1
     assert kvb.heads_per_workgroup(kvb.Shape(2, 56, 8, 128)) == 7
     assert kvb.heads_per_workgroup(kvb.Shape(1, 16, 1, 128), "f32") == 8
-    assert kvb.heads_per_workgroup(kvb.Shape(1, 16, 1, 128), "i8") == 8
+    assert kvb.heads_per_workgroup(kvb.Shape(1, 16, 1, 128), "i8") == 16
     assert kvb.heads_per_workgroup(kvb.Shape(1, 16, 1, 128), "f16") == 16
+    assert kvb.heads_per_workgroup(kvb.Shape(1, 64, 1, 128), "i8") == 32
 
 
 def test_partition_policy_counts_live_heads(kvb):
