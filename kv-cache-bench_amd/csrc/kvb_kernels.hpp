@@ -22,23 +22,21 @@ constexpr int kTile = 16;
 // The waves of a paged_decode workgroup that serves qg query heads of one KV head: qw heads per
 // wave, ts token streams (stream s walks the partition's 32-token tiles s, s + ts, ...) and hs head
 // splits (the waves of split j serve heads j * qw .. j * qw + qw - 1 and walk the same tiles as the
-// other splits' waves of their stream), hs * ts waves in all. Up to 8 heads (16 for fp16, two
-// 8-head blocks per wave) one wave serves every head: four streams, one wave per SIMD, the
-// reference's kSimdGroups. Past that the splits read each page once from HBM and again from the CU's
-// own caches, where the sibling workgroups of one KV head, each on its own CU, read it again from
-// L2 (MI355X, 4 x 32k tokens, 8 KV heads, page 128: int8 with 16 query heads per KV head 84.0 us as
-// two 8-head workgroups; fp16 with 32, 132.2 us as two 16-head workgroups; int8 with 32, 122.7 us).
-//  * int8, 16 heads: two splits of four streams, 8 waves (two per SIMD, each wave's registers as at
-//    8 heads); each split gives the bits of an 8-head workgroup.
-//  * int8, 32 heads: four splits of two streams, 8 waves.
-//  * fp16, 32 heads: two splits of two streams of 16-head waves, 4 waves (one per SIMD: a 16-head
-//    wave holds about 360 registers).
+// other splits' waves of their stream), hs * ts waves in all.
+//  * Up to 16 heads (fp32: 8) one wave serves every head: four streams, one wave per SIMD, the
+//    reference's kSimdGroups (16 heads: one head per MFMA column, fp16 and int8).
+//  * 32 heads: two splits of four streams of 16-head waves, 8 waves, two per SIMD. int8 waves read
+//    each tile themselves, the second split mostly from the CU's caches; the two fp16 waves of a
+//    stream load half a tile each and share it through LDS (SHL in paged_decode_kernel).
+// (MI355X, 4 x 32k tokens, 8 KV heads, page 128, before head splits: int8 with 16 query heads per KV
+// head 84.0 us as two 8-head workgroups; fp16 with 32, 132.2 us as two 16-head workgroups; int8
+// with 32, 122.7 us as four 8-head workgroups.)
 struct DecodeShape {
     int qw, hs, ts;
 };
 constexpr DecodeShape decode_shape(int kind, int qg) {
     if (kind == KV_I8 && qg == 32) return DecodeShape{16, 2, 4};
-    if (kind == KV_F16 && qg == 32) return DecodeShape{16, 2, 2};
+    if (kind == KV_F16 && qg == 32) return DecodeShape{16, 2, 4};
     return DecodeShape{qg, 1, decode_waves(kind)};
 }
 constexpr int decode_wg_waves(int kind, int qg) { return decode_shape(kind, qg).hs * decode_shape(kind, qg).ts; }

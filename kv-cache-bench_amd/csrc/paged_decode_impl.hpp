@@ -337,10 +337,10 @@ __device__ __forceinline__ WorkItem ragged_item(const int32_t* seq_lens, int bat
 // partitions' tiles in order; each partition's tiles go to the same waves, in the same order, as in
 // a workgroup of its own (part_tokens is a multiple of 32 * waves), and a wave starts its second
 // partition from a fresh state, so every partition gets the same bits either way.
-// QG is the workgroup's query heads. Past 8 (fp16: 16) its waves split them (decode_shape: QW heads
-// per wave, HS head splits of TS token streams): a wave walks its stream's tiles for its split's
-// heads, so each tile is read by HS waves, the first from HBM and the others mostly from the CU's
-// caches, with ordinary loads.
+// QG is the workgroup's query heads. Past 16 its waves split them (decode_shape: QW heads per wave,
+// HS head splits of TS token streams): a wave walks its stream's tiles for its split's heads. int8:
+// each tile is read by HS waves, the first from HBM and the others mostly from the CU's caches, with
+// ordinary loads; fp16: the stream's two waves load half a tile each and share it through LDS (SHL).
 template <int KIND, int D, int QG, bool FAST, bool LOADS = false, bool PAIR = false, bool PART = false,
           bool SHARE = false, bool STAGE = false>
 __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdgpu_waves_per_eu(
@@ -374,6 +374,16 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
     // head's max grows on most tiles (about 27 of a c4 wave's 32). 8-head waves rescale eagerly.
     constexpr bool LAZY = COLH;
     constexpr float kLazyRescale = 8.0f;
+    // SHL (fp16, two head splits): the two waves of a stream share each tile through LDS. The first
+    // split's wave loads the tile's K rows, the second's its V rows, each into a half-tile register
+    // buffer (32 VGPRs at head_dim 128 where a whole tile takes 64); both write their half to the
+    // stream's LDS slot (two per stream, alternating), meet at the stream's LDS counter, and compute
+    // the tile from the slot. Each tile is read from HBM once, two tiles are in flight per stream,
+    // and the registers left free fit four streams at two waves per SIMD. (Read by each split from
+    // the CU's caches instead, four streams of fp16 tiles at head_dim 128 outgrew them and the second
+    // reads went back to HBM: 165 us at 4 x 32k tokens with 32 query heads per KV head, against 108
+    // for two streams.)
+    constexpr bool SHL = HS == 2 && KIND == KV_F16;
     // Tile register buffers per wave: one computed while the next is loaded (see the tile walk).
     // fp32 tiles are too large for more than one. (Three for int8, whose tiles are half an fp16
     // tile, spill at head_dim 128 and measured slower.)
@@ -382,13 +392,18 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
     // with SHARE, whose sibling workgroups read each page again from L2 (MI355X, c4's size with
     // groups of 16: 163.5 -> 106.9 us fp16, 88.2 -> 68.0 int8, against 133.7 / 80.9 with the sibling
     // order alone; non-temporal stays for one workgroup per KV head: 84.5 us there, 93.9 without).
-    // Head splits (HS > 1) read each tile once per split: ordinary loads, as SHARE.
-    constexpr int kKvPolicy = SHARE || HS > 1 ? 0 : kNonTemporal;
+    // Head splits (HS > 1) read each tile once per split: ordinary loads, as SHARE (SHL: once).
+    constexpr int kKvPolicy = SHARE || (HS > 1 && !SHL) ? 0 : kNonTemporal;
 
     // Per wave: the V tile (32 rows of D elements, swizzled); after the loop it holds the wave's
     // final accumulators [HQ][D] fp32 for the merge (every head row is written, the ones past qg
     // unread): the larger of the two.
-    constexpr int SVB = kTok * T::LDS_ESZ >= HQ * 4 ? kTok * D * T::LDS_ESZ : HQ * D * 4;
+    // SHL: [W][one tile's K and V]: the two slots of stream s are s_v[2 s] and s_v[2 s + 1] (K rows
+    // as loaded, lane-major, then the V tile), and wave w's final accumulators go to s_v[w] after the
+    // walk.
+    constexpr int SKB = kTok * D * T::LDS_ESZ;  // SHL: the K half of a slot
+    constexpr int SVB = SHL ? (2 * SKB >= HQ * D * 4 ? 2 * SKB : HQ * D * 4)
+                            : kTok * T::LDS_ESZ >= HQ * 4 ? kTok * D * T::LDS_ESZ : HQ * D * 4;
     __shared__ __attribute__((aligned(16))) unsigned char s_v[W][SVB];
     __shared__ float2 s_ml[W][QW];
     __shared__ float s_mt[LAZY ? W : 1][QW];  // LAZY: each wave's true max per head
@@ -610,6 +625,65 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
                                                               rvh[h], (i * (64 / VL) + lane / VL) * D * T::ESZ + (lane % VL) * 16, 0, kKvPolicy));
     };
 
+    // ---- SHL: this wave's half of a tile, K rows (split 0) or V rows (split 1), into x[h][m]: the
+    // rows and buffer ranges of load_tile, each lane's row and byte of the one or the other (for
+    // fp16 a half tile takes as many 16-byte loads of K as of V). Past t1 it reads zeros.
+    constexpr int NL = T::KLOADS;
+    static_assert(!SHL || T::NV == T::KLOADS, "SHL: equal K and V loads");
+    const int split = HS == 1 ? 0 : wave / TS;
+    const char* hbase = split ? vbase : kbase;
+    auto hrow = [&](int m) { return split ? m * (64 / VL) + lane / VL : c; };              // row of the half tile
+    auto hcol = [&](int m) { return split ? (lane % VL) * 16 : T::kdoff(m, q4) * T::ESZ; };  // its byte
+    auto load_half = [&](uint4 (&x)[2][NL], int tt) {
+        int braw = 0, off = 0;
+        for (int h = 0; h < 2; ++h) {
+            const int th = tt + h * kHalf;
+            if constexpr (FAST) {  // (load_tile's rows and range)
+                const int tc = min(th, t1 - 1);
+                if (h == 0 || !p.tile_in_page) {
+                    const int bi = fast_div(tc, p.page_div);
+                    braw = lanes ? lane_block(bi - bi0) : bt[bi];
+                    off = tc - bi * P;
+                } else {
+                    off += kHalf;
+                }
+                const size_t row0 = ((size_t)max(braw, 0) * Hkv + kvh) * P + off;
+                const int rows = braw < 0 ? 0 : max(0, __builtin_amdgcn_readfirstlane(min(kHalf, t1 - th)));
+                const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<char*>(hbase + row0 * D * T::ESZ), (short)0, rows * D * T::ESZ, 0x00020000);
+                for (int m = 0; m < NL; ++m)
+                    x[h][m] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                            rh, hrow(m) * D * T::ESZ + hcol(m), 0, kKvPolicy));
+            } else {
+                for (int m = 0; m < NL; ++m) {
+                    const int tk = th + hrow(m);
+                    const int tks = tk < t1 ? tk : t0;
+                    const int bi = fast_div(tks, p.page_div);
+                    const int id = block_of(bi);
+                    const size_t row = ((size_t)max(id, 0) * Hkv + kvh) * P + (tks - bi * P);
+                    const uint4 v = *reinterpret_cast<const uint4*>(hbase + row * D * T::ESZ + hcol(m));
+                    x[h][m] = tk < t1 && id >= 0 ? v : make_uint4(0, 0, 0, 0);
+                }
+            }
+        }
+    };
+    // the half into the slot: K lane-major (each lane reads back its own offsets), V as store_v
+    // lays it out
+    auto put_half = [&](unsigned char* slot, const uint4 (&x)[2][NL]) {
+        if constexpr (SHL)
+            for (int h = 0; h < 2; ++h)
+                for (int m = 0; m < NL; ++m) {
+                    int o;
+                    if (split == 0) {
+                        o = ((h * NL + m) * 64 + lane) * 16;
+                    } else {
+                        const int t = h * kHalf + m * (64 / VL) + lane / VL;
+                        o = SKB + t * D * T::LDS_ESZ + 16 * ((lane % VL) ^ T::vswz(t));
+                    }
+                    *reinterpret_cast<u32x4_t*>(slot + o) = __builtin_bit_cast(u32x4_t, x[h][m]);
+                }
+    };
+
     // ---- q as the B operand of S^T = K Q^T: column c holds head c/2, high (c even) or low part;
     // COLH, head c, whose high and low parts (int8: digits) go to separate MFMAs.
     // Its loads go out first, then the wave's first NBUF - 1 tiles; the q split then runs under
@@ -642,13 +716,21 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
 
     const int ntiles = (t1 - t0 + kTok - 1) / kTok;
     int it = stream;
-    R r[NBUF];
-    for (int k = 0; k + 1 < NBUF; ++k) {
-        load_tile(r[k], t0 + (it + k * TS) * kTok);
-        // (in buffer order, as the loop issues them: the loop head is entered from here and from the
-        // back edge, and the wait for buffer 0 there can leave the later buffers in flight only if
-        // both paths issued them in the same order)
-        __builtin_amdgcn_sched_barrier(0);
+    R r[SHL ? 1 : NBUF];
+    uint4 x[SHL ? 2 : 1][2][NL];  // SHL: the stream's next two tiles, this wave's halves
+    if constexpr (SHL) {
+        for (int k = 0; k < 2; ++k) {
+            load_half(x[k], t0 + (it + k * TS) * kTok);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+        for (int k = 0; k + 1 < NBUF; ++k) {
+            load_tile(r[k], t0 + (it + k * TS) * kTok);
+            // (in buffer order, as the loop issues them: the loop head is entered from here and from the
+            // back edge, and the wait for buffer 0 there can leave the later buffers in flight only if
+            // both paths issued them in the same order)
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     // (an empty asm with a memory clobber: without it the tile loads are sunk past the q split, to
     // their first use, and the q loads past the tiles')
@@ -786,7 +868,7 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
             (void)tt;
             return;
         }
-        store_v(r);
+        if constexpr (!SHL) store_v(r);  // (SHL: the tile is in LDS already)
         // S^T = K Q^T for both halves. S[a][h]: a = 0 the column's part (COLH: the high part,
         // int8 d0 + d2 / 2^14), a = 1 (COLH) the low part (int8 d1 / 2^7): the values columns 2h and
         // 2h + 1 hold in the two-column layout.
@@ -1005,6 +1087,57 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
     // tile of the second partition the wave moves its state to s_part and starts afresh.
     int cur = 0;
     const int tpp = p.part_tokens / kTok;  // tiles per partition
+    if constexpr (SHL) {
+        // Step j: the wave's half of tile j (two steps old) goes to slot j % 2, the half of tile j + 2
+        // is issued into its registers, and once both waves of the stream have written their halves
+        // both compute tile j from the slot. The two meet at the stream's counter in LDS: each adds
+        // its arrival (a release: its slot writes complete first) and waits until the count holds
+        // both arrivals of this step (an acquire: its slot reads follow). Slot j % 2 was last read at
+        // step j - 2, before the wave's arrival at step j - 1, which the other wave waited for before
+        // writing the slot again. Both waves take the same steps (their stream's tiles, in whole
+        // pairs; the last pair may step past the last tile, reading zeros, and computes nothing
+        // there), and each adds before it waits, so every wait ends. Only the two waves of a stream
+        // wait for each other: with a workgroup barrier at every step instead, each step waited for
+        // the slowest of the four streams (98.1-101.6 us against 92.3-94.3 at 4 x 32k tokens with 32
+        // query heads per KV head).
+        __shared__ unsigned s_pair[SHL ? TS : 1];
+        if (threadIdx.x < TS) s_pair[threadIdx.x] = 0u;
+        __syncthreads();
+        const int wt = it < ntiles ? (ntiles - it + TS - 1) / TS : 0;
+        unsigned want = 0;
+        for (int rd = 0; rd < (wt + 1) / 2; ++rd) {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                if constexpr (LOADS) {  // the same loads, consumed by XORs; nothing shared or computed
+                    for (int h = 0; h < 2; ++h)
+                        for (int m = 0; m < NL; ++m) lsink ^= x[k][h][m].x ^ x[k][h][m].y ^ x[k][h][m].z ^ x[k][h][m].w;
+                    load_half(x[k], t0 + (it + 2 * TS) * kTok);
+                    __builtin_amdgcn_sched_barrier(0);
+                    it += TS;
+                    continue;
+                }
+                unsigned char* slot = s_v[2 * stream + k];
+                put_half(slot, x[k]);
+                load_half(x[k], t0 + (it + 2 * TS) * kTok);
+                __builtin_amdgcn_sched_barrier(0);
+                __hip_atomic_fetch_add(&s_pair[stream], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                want += 128;  // (each of the two waves' 64 lanes adds 1)
+                while (__hip_atomic_load(&s_pair[stream], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < want)
+                    __builtin_amdgcn_s_sleep(1);
+                if (it < ntiles) {  // uniform over the stream's two waves
+                    R rr{};  // (K only: fp16 has no scales, and rel is read only for them)
+                    for (int h = 0; h < 2; ++h)
+                        for (int m = 0; m < NL; ++m)
+                            rr.k[h][m] = *reinterpret_cast<const uint4*>(slot + ((h * NL + m) * 64 + lane) * 16);
+                    vt = slot + SKB;
+                    compute_tile(rr, t0 + it * kTok);
+                }
+                it += TS;
+            }
+        }
+        vt = s_v[wave];
+        __syncthreads();  // every slot is read before the waves' states overwrite them
+    } else {
     const int wtiles = it < ntiles ? (ntiles - it + TS - 1) / TS : 0;
     const int rounds = (wtiles + NBUF - 1) / NBUF;
     for (int rd = 0; rd < rounds; ++rd) {
@@ -1029,6 +1162,7 @@ __global__ __launch_bounds__(64 * decode_wg_waves(KIND, QG)) __attribute__((amdg
             compute_tile(r[k], t0 + it * kTok);
             it += TS;
         }
+    }
     }
 
 #ifdef KVB_WG_TIMESTAMPS

@@ -528,8 +528,11 @@ typedef ::kvbemu::BufferRsrc __amdgpu_buffer_rsrc_t;
 // ordering hints with no CPU meaning: a fiber's own memory operations complete in program order
 #define __builtin_amdgcn_fence(...) ((void)0)
 #define __builtin_amdgcn_sched_barrier(...) ((void)0)
+// s_sleep in a wait loop: the other fibers of the workgroup run meanwhile
+#define __builtin_amdgcn_s_sleep(n) ::kvbemu::yield()
 #define __hip_atomic_fetch_add(p, v, order, scope) ::kvbemu::atomic_fetch_add((p), (v))
-#define __hip_atomic_load(p, order, scope) (*(p))
+// (volatile: a wait loop reads the value again after other fibers ran)
+#define __hip_atomic_load(p, order, scope) (*(volatile std::remove_reference_t<decltype(*(p))>*)(p))
 #define __hip_atomic_store(p, v, order, scope) ((void)(*(p) = (v)))
 #define HIP_SYMBOL(x) (::kvbemu::symbol(&(x)))
 

@@ -156,6 +156,19 @@ MUTANTS = [
       "const int hw0 = HS == 1 ? h0 : h0 + (wave / TS) * QW;", "const int hw0 = h0;"),
     X("head splits: the wave merge takes the first split's waves for every head",
       "const int w0 = HS == 1 ? 0 : (eh / QW) * TS,", "const int w0 = 0,"),
+    # fp16 head splits sharing tiles through LDS (SHL)
+    X("shared tiles: both waves of a stream load the K rows",
+      "const char* hbase = split ? vbase : kbase;", "const char* hbase = kbase;"),
+    X("shared tiles: the second half tile reads the first half's rows",
+      "} else {\n                    off += kHalf;\n                }\n                const size_t row0 = ((size_t)max(braw, 0)",
+      "} else {\n                    off += 0;\n                }\n                const size_t row0 = ((size_t)max(braw, 0)"),
+    X("shared tiles: the V half written without its swizzle",
+      "o = SKB + t * D * T::LDS_ESZ + 16 * ((lane % VL) ^ T::vswz(t));", "o = SKB + t * D * T::LDS_ESZ + 16 * (lane % VL);"),
+    X("shared tiles: K read back from the slot in another order",
+      "rr.k[h][m] = *reinterpret_cast<const uint4*>(slot + ((h * NL + m) * 64 + lane) * 16);",
+      "rr.k[h][m] = *reinterpret_cast<const uint4*>(slot + ((m * 2 + h) * 64 + lane) * 16);"),
+    X("shared tiles: a wave waits for its own arrival only",
+      "want += 128;", "want += 64;"),
     X("fp16 q: low column dropped (q as one fp16 number)",
       "aq16[0][j][s] = hl ? lo : hi;", "aq16[0][j][s] = hl ? (_Float16)0.0f : hi;"),
     X("fp16 q, 16-head waves: low parts dropped",
@@ -197,9 +210,11 @@ MUTANTS = [
     X("tile-aligned pages: K and V one row later inside the page",
       "const size_t row0 = ((size_t)blk * Hkv + kvh) * P + off;",
       "const size_t row0 = ((size_t)blk * Hkv + kvh) * P + off + 1;"),
-    X("tile-aligned pages: the second half tile reads the first half's rows", "off += kHalf;", "off += 0;"),
+    X("tile-aligned pages: the second half tile reads the first half's rows",
+      "r.rel[h] = r.rel[0];\n                    off += kHalf;", "r.rel[h] = r.rel[0];\n                    off += 0;"),
     X("the partition's first block for every tile (block ids in lanes)",
-      "braw = lanes ? lane_block(bi - bi0) : bt[bi];", "braw = lanes ? lane_block(0) : bt[bi];"),
+      "r.rel[h] = bi - bi0;\n                    braw = lanes ? lane_block(bi - bi0) : bt[bi];",
+      "r.rel[h] = bi - bi0;\n                    braw = lanes ? lane_block(0) : bt[bi];"),
     X("any page size: V one row later inside the page",
       "* P + (tvs - vbi * P);", "* P + (tvs + 1 - vbi * P) % P;"),
     X("wave merge weight exp(M - m) instead of exp(m - M)",

@@ -3,8 +3,9 @@ kvb_heads_per_workgroup query heads of a KV head: 16 or 32 where they divide the
 int8), else the largest divisor of the group that is at most 8, so it reads each K/V page once for
 all of them (src/metal_attn.mm:64-80 builds its kernel with QG = GROUP for any group). Up to 8
 heads it runs the kernel built for the next of 1, 2, 4 and 8 heads, whose MFMA columns past those
-heads stay idle; 16 and 32 heads are split over the workgroup's waves. Checked for every storage
-type:
+heads stay idle; 16 heads run as one 16-head wave per token stream, 32 as two head splits of
+16-head waves (fp16: the two waves of a stream share each tile through LDS, one loading its K rows
+and the other its V rows). Checked for every storage type:
 - the output against the oracle, on the plain grid (fused merge, one and two partitions per
   workgroup), the ragged grid, and a layout whose page is not a tile multiple;
 - the fused step against the two-kernel form, bit for bit;
@@ -31,8 +32,8 @@ SHAPES = [
     ((1, 24, 2, 128), 6),   # group 12: two workgroups per KV head
     ((1, 28, 2, 64), 7),    # group 14: two workgroups per KV head
     ((1, 18, 2, 64), 3),    # group 9: three workgroups of 3 per KV head
-    ((1, 32, 2, 128), 16),  # group 16: f16 two 8-head blocks per wave, i8 two head splits (f32: two of 8)
-    ((1, 64, 2, 128), 32),  # group 32: f16 two splits of 16-head waves, i8 four splits (f32: four of 8)
+    ((1, 32, 2, 128), 16),  # group 16: 16-head waves (f32: two workgroups of 8)
+    ((1, 64, 2, 128), 32),  # group 32: two head splits of 16-head waves, f16 sharing tiles (f32: four of 8)
     ((2, 32, 1, 64), 32),   # group 32, one KV head, head_dim 64
 ]
 IDS = [f"H{s[1]}-Hkv{s[2]}-D{s[3]}" for s, _ in SHAPES]
