@@ -18,8 +18,10 @@
 #endif
 #endif
 
+#include <algorithm>
 #include <chrono>
 #include <cstdarg>
+#include <cstdlib>
 #include <map>
 #include <string>
 #include <vector>
@@ -74,6 +76,12 @@ std::string g_msg;           // its message
 std::string g_last_msg;      // the last launch error's message (kvbemu_last_error)
 hipError_t g_last_err = hipSuccess;
 std::vector<Fiber> g_fibers;
+// the seed of the wave order (KVBEMU_SEED, default 1)
+const uint64_t g_seed = [] {
+    const char* e = std::getenv("KVBEMU_SEED");
+    const uint64_t s = e ? std::strtoull(e, nullptr, 0) : 1;
+    return s ? s : 1;
+}();
 std::vector<char*> g_stacks;
 std::map<uintptr_t, size_t> g_allocs;  // base -> bytes: hipMalloc and registered symbols
 #ifdef KVBEMU_ASAN
@@ -231,6 +239,8 @@ hipError_t launch(dim3 grid, dim3 block, const std::function<void()>& body) {
     g_fibers.assign((size_t)threads, Fiber{});
     const int nw = (int)((threads + 63) / 64);
     std::vector<WaveSync> waves((size_t)nw);
+    std::vector<int> order((size_t)nw);
+    for (int w = 0; w < nw; ++w) order[w] = w;
     Group grp;
     grp.grid = Idx{grid.x, grid.y, grid.z};
     grp.block = Idx{block.x, block.y, block.z};
@@ -262,14 +272,27 @@ hipError_t launch(dim3 grid, dim3 block, const std::function<void()>& body) {
                     f.sp = init_context(f.stack);
                 }
                 g_grp = &grp;
+                // Each pass over the workgroup takes its waves in a fresh order (xorshift from a fixed
+                // seed, KVBEMU_SEED to change it), the lanes of a wave in order: waves then meet only
+                // where the kernel makes them (barriers, counters in LDS), not because a lower wave
+                // always runs first.
+                uint64_t rng = g_seed ^ (0x9E3779B97F4A7C15ull * (1 + bx + grid.x * (by + (uint64_t)grid.y * bz)));
                 while (grp.live > 0 && !g_failed) {
                     const uint64_t before = grp.progress;
-                    for (Fiber& f : g_fibers) {
-                        if (f.done) continue;
-                        g_cur = &f;
-                        switch_to_fiber(f);
-                        if (g_failed) break;
+                    for (int i = nw - 1; i > 0; --i) {
+                        rng ^= rng << 13;
+                        rng ^= rng >> 7;
+                        rng ^= rng << 17;
+                        std::swap(order[i], order[rng % (uint64_t)(i + 1)]);
                     }
+                    for (int wi = 0; wi < nw && !g_failed; ++wi)
+                        for (int t = 64 * order[wi]; t < std::min(64 * order[wi] + 64, (int)threads); ++t) {
+                            Fiber& f = g_fibers[t];
+                            if (f.done) continue;
+                            g_cur = &f;
+                            switch_to_fiber(f);
+                            if (g_failed) break;
+                        }
                     if (!g_failed && grp.live > 0 && grp.progress == before) {
                         char buf[200];
                         std::snprintf(buf, sizeof buf,

@@ -486,6 +486,7 @@ template <class T, class U>
 T atomic_fetch_add(T* p, U v) {
     const T o = *p;
     *p = (T)(o + (T)v);
+    if (g_grp) ++g_grp->progress;  // (another fiber may be waiting for it)
     return o;
 }
 

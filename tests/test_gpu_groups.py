@@ -177,6 +177,43 @@ def test_sibling_workgroups_give_group8_bits(gpu, kv, lens, part):
 
 
 @pytest.mark.parametrize("kv", ["f16", "i8"])
+def test_sixteen_head_waves_keep_each_eight_heads_precision(gpu, kv):
+    """A 16-head wave takes q's power-of-two scale per 8 heads (fp16; int8 per head), as two 8-head
+    waves would. Heads 0-7 of each group with |q| near 2^10 and heads 8-15 near 2^-12, over K near
+    2^10 so that the small heads' scores still spread their softmax: one scale for all 16 would put
+    the small heads' low fp16 parts among the subnormals (about 1e-5 in their p). Each 8 of the 16
+    heads against a group-8 run of the same heads, to fp32 rounding (2e-7 of max(1, max |v|))."""
+    kvb = gpu
+    rng = np.random.default_rng(2026 + len(kv))
+    B, H, Hkv, D, lens = 2, 32, 2, 128, [700, 333]
+    q = rng.standard_normal((B, H, D)).astype(np.float32)
+    for g in range(H // 16):
+        q[:, 16 * g:16 * g + 8] *= 2.0 ** 10
+        q[:, 16 * g + 8:16 * g + 16] *= 2.0 ** -12
+    k = (rng.standard_normal((B, Hkv, max(lens), D)) * 2.0 ** 10).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, max(lens), D)).astype(np.float32)
+    w16 = kvb.Workload.from_arrays(kv, lens, q, k, v)
+    assert kvb.heads_per_workgroup(w16.shape, kv) == 16
+    c16 = kvb.PagedCache(w16, 16, 3, pool_factor=1.5, poison=True)
+    dev = kvb.DeviceCase(w16, c16)
+    dev.run(256)
+    out16 = dev.output().copy()
+    dev.free()
+    vmax = float(np.abs(c16.dequantized(w16)[1] if kv == "i8" else w16.v.astype(np.float32)).max())
+    for half in (0, 1):
+        heads = [16 * g + 8 * half + j for g in range(H // 16) for j in range(8)]
+        w8 = kvb.Workload.from_arrays(kv, lens, q[:, heads], w16.k, w16.v)
+        c8 = kvb.PagedCache(w8, 16, 5, pool_factor=1.5, poison=True)
+        d8 = kvb.DeviceCase(w8, c8)
+        d8.run(256)
+        out8 = d8.output()
+        d8.free()
+        d = float(np.abs(out16[:, heads] - out8).max())
+        progress(f"[groups] {kv} heads of 2^10 and 2^-12 in one 16-head wave, half {half}: max |diff| {d:.3g}")
+        assert d <= 2e-7 * max(1.0, vmax), half
+
+
+@pytest.mark.parametrize("kv", ["f16", "i8"])
 @pytest.mark.parametrize("heads,dim", [(32, 128), (64, 128), (64, 64)], ids=["g16", "g32", "g32-D64"])
 def test_wide_groups_past_sixteen_partitions(gpu, oracle, kv, heads, dim):
     """16 and 32 heads per workgroup past 16 partitions. The fused merge of more than 16 gives each
@@ -199,3 +236,60 @@ def test_wide_groups_past_sixteen_partitions(gpu, oracle, kv, heads, dim):
         assert np.array_equal(fused.view(np.uint32), split.view(np.uint32)), part
         err = pb.check_output(kvb, oracle, w, c, fused)
         progress(f"[groups] {heads // 2} heads, D {dim}, {kv}, part {part}: max err {err:.3g}")
+
+
+# (B, H, Hkv, D), lengths, page, partitions
+LONG_CASES = [
+    ((2, 64, 2, 128), [4000, 2333], 16, (1024, 2048, 4096)),
+    ((2, 64, 1, 64), [3000, 17], 128, (1024, 3072)),
+    ((1, 128, 2, 128), [2500], 64, (1024, 2048)),  # group 64: two 32-head workgroups per KV head
+    ((2, 64, 2, 128), [1500, 900], 24, (512, 1024)),  # a page that is not a multiple of 16
+]
+
+
+@pytest.mark.parametrize("kv", ["f16", "i8"])
+@pytest.mark.parametrize("case", range(len(LONG_CASES)))
+def test_shared_tiles_long_partitions(gpu, oracle, case, kv):
+    """Groups of 32 and 64 over partitions of up to eight tiles per stream, whose streams end their
+    walks at different steps (fp16: the two head splits of a stream share each tile through LDS,
+    the stream's two slots reused round after round). Against the oracle; fused equal to
+    two-kernel."""
+    kvb = gpu
+    shape, lens, page, parts = LONG_CASES[case]
+    w = kvb.Workload(kvb.Shape(*shape), kv, lens, seed=501 + case, varied=(kv == "i8"))
+    assert kvb.heads_per_workgroup(w.shape, kv) == 32
+    c = kvb.PagedCache(w, page, 11 * page + case, pool_factor=1.5, poison=True)
+    for part in parts:
+        dev = kvb.DeviceCase(w, c)
+        dev.out.fill(0xFF)
+        dev.run(part)
+        fused = dev.output().copy()
+        dev.out.fill(0xFF)
+        dev.run_split(part)
+        split = dev.output().copy()
+        dev.free()
+        assert np.array_equal(fused.view(np.uint32), split.view(np.uint32)), part
+        err = pb.check_output(kvb, oracle, w, c, fused)
+        progress(f"[shared tiles] {kv} {shape} lens {lens} page {page} part {part}: max err {err:.3g}")
+
+
+@pytest.mark.parametrize("kv", ["f16", "i8"])
+@pytest.mark.parametrize("heads", [32, 64])
+def test_loads_only_wide_groups(gpu, kv, heads):
+    """kvb_run_paged_loads on 16- and 32-head workgroups (fp16 32: the shared tiles' half-tile
+    loads) reports a GPU time, leaves the output untouched, and a decode step afterwards is
+    unchanged."""
+    kvb = gpu
+    w = kvb.Workload(kvb.Shape(2, heads, 2, 128), kv, [2048, 700], seed=61 + heads)
+    c = kvb.PagedCache(w, 16, 7, pool_factor=1.5)
+    dev = kvb.DeviceCase(w, c)
+    dev.run(512)
+    want = dev.output()
+    dev.out.fill(0x7F)
+    sentinel = dev.output()
+    progress(f"[shared tiles] loads-only {kv} {heads // 2} heads per workgroup")
+    assert dev.run_loads(512) > 0
+    assert np.array_equal(dev.output(), sentinel, equal_nan=True)
+    dev.run(512)
+    assert np.array_equal(dev.output(), want)
+    dev.free()
