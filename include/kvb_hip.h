@@ -123,8 +123,9 @@ size_t kvb_paged_workspace_bytes(const kvb_paged_args* a);
  * otherwise the largest divisor of the group that is at most 8 (a group of 7 is one workgroup per
  * KV head, a group of 12 two of 6, a group of 64 two of 32); without share_kv, 1. The reference's
  * kernel serves the whole group from one threadgroup (QG = GROUP, src/metal_attn.mm:64-80); here
- * the score MFMA holds 8 heads, a wave runs one block of them (two for f16), and a workgroup of 16
- * or 32 heads splits them over its waves, which walk the same tiles. Returns -1 on bad arguments
+ * a wave's score MFMA holds up to 8 heads in two columns each, or 16 in one column each (f16, i8),
+ * and a workgroup of 32 heads splits them over two sets of waves that walk the same tiles (f16:
+ * each tile loaded once and shared through LDS). Returns -1 on bad arguments
  * (num_kv_heads <= 0, num_heads not a positive multiple of it, kv_type not a kvb_kv_type). */
 int kvb_heads_per_workgroup(int num_heads, int num_kv_heads, int kv_type, int share_kv);
 
