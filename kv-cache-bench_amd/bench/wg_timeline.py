@@ -15,13 +15,14 @@ the arrival count, and (merging workgroups) the merge; and the time from the las
 A second table follows the workgroup that ended last through the same steps (the step's critical
 path). Median over 5 launches after 1 discarded. Prints markdown tables per configuration.
 
-With --warm, no flush before the launches (caches and the previous launch as a decode loop leaves
+With --heads=H, each configuration runs with H query heads (its KV heads, batch and lengths
+unchanged), for the wide GQA groups. With --warm, no flush before the launches (caches and the previous launch as a decode loop leaves
 them). With --where, also where the workgroups ran (wave 0's HW_ID and XCC_ID, stamped by the same build),
 for the last launch of each form: loop durations and loop ends per XCD, and per rank of a workgroup
 among those that ran on the same CU (by start time), which separates a CU's first workgroup from the
 ones that shared or followed it.
 
-usage: python3 kv-cache-bench_amd/bench/wg_timeline.py [--where] [--warm] c2 [c3 c4 c5i8 ...]
+usage: python3 kv-cache-bench_amd/bench/wg_timeline.py [--where] [--warm] [--heads=H] c2 [c3 c4 c5i8 ...]
 """
 from __future__ import annotations
 
@@ -132,6 +133,8 @@ def summarise(kvb, dev, part, mode, read, reps=6, where=None, warm=False):
 
 def main(args):
     show_where = "--where" in args
+    heads = next((int(a.split("=", 1)[1]) for a in args if a.startswith("--heads=")), 0)
+    args = [a for a in args if not a.startswith("--heads=")]
     warm = "--warm" in args
     configs = [a for a in args if a not in ("--where", "--warm")] or ["c2"]
     kvb = graft.load_package()
@@ -139,12 +142,16 @@ def main(args):
         sys.exit("wg_timeline: no GPU")
     print(f"device: {kvb.device_name()}; us, relative to the launch's first workgroup start\n")
     for cfg in configs:
+        if heads:
+            s = kvb.CONFIGS[cfg]["shape"]
+            kvb.CONFIGS[cfg] = dict(kvb.CONFIGS[cfg], shape=kvb.Shape(s.batch, heads, s.num_kv_heads, s.head_dim))
         w, c, cfgd = kvb.make_config(cfg, threads=16)
         part = kvb.config_part(cfgd, w)
         read = getattr(kvb.hip, "kvb_wg_stamps_" + kvb.KV_NAMES[w.kv_type])
         read.argtypes, read.restype = [ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int
         dev = kvb.DeviceCase(w, c)
-        print(f"### {cfg}: partition {part}, {int(w.lens.sum())} tokens\n")
+        with_heads = f" with {heads} query heads" if heads else ""
+        print(f"### {cfg}{with_heads}: partition {part}, {int(w.lens.sum())} tokens\n")
         print("| launch | " + " | ".join(h for _, h in COLUMNS) + " |")
         print("|---" * (len(COLUMNS) + 1) + "|")
         wheres, last = {}, {}
